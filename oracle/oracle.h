@@ -1,0 +1,168 @@
+/*
+ * oracle.h — CPU restatement of RIE's per-token forward loop (x86 path).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
+ * entry point and the CPU-baseline leg of bench.py may load it; the product
+ * (rust_interference_engine_amd) never links, calls or falls back to it.
+ *
+ * Every function restates the reference algorithm it names (file:line in the
+ * reference tree crates/rie-core/src/...), including the rounding and the
+ * accumulation order of the x86 AVX2 kernels RIE selects on an x86 host, so
+ * that integer results (activation codes, block dots, KV codes) are bit-exact
+ * and float results follow the same operation order.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; fused multiply-adds only
+ * where the reference uses _mm256_fmadd_ps, written as explicit fmaf()).
+ */
+#ifndef RIE_ORACLE_H
+#define RIE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, quant/mod.rs:34-51 */
+enum {
+    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7,
+    OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13,
+    OR_Q6_K = 14, OR_BF16 = 30
+};
+
+/* activation formats, quant/mod.rs:127-132 */
+enum { OR_ACT_F32 = 0, OR_ACT_Q8_0 = 1, OR_ACT_Q8K = 2 };
+
+/* KV cache formats, model/cpu.rs:12-25 */
+enum { OR_KV_F16 = 0, OR_KV_Q8_0 = 1, OR_KV_TURBO4 = 2 };
+
+/* BlockQ8_0, quant/mod.rs:141-147 (repr(C, align(16)): 48 bytes) */
+typedef struct __attribute__((aligned(16))) {
+    int8_t qs[32];
+    float d;
+    float s;
+} or_block_q8_0;
+
+/* BlockQ8K, quant/mod.rs:156-162 (repr(C, align(16)): 304 bytes) */
+typedef struct __attribute__((aligned(16))) {
+    int8_t qs[256];
+    int16_t bsums[16];
+    float d;
+} or_block_q8k;
+
+/* ---- scalar helpers ---------------------------------------------------- */
+uint16_t or_f32_to_f16(float x);          /* IEEE round-to-nearest-even (half 2.7.1 from_f32) */
+float or_f16_to_f32(uint16_t h);          /* exact */
+uint16_t or_f32_to_bf16(float x);         /* half 2.7.1 bf16::from_f32 (RNE) */
+void or_f32_to_f16_slice(const float *src, uint16_t *dst, size_t n);
+
+/* xorshift Rng, testing.rs:10-30 */
+typedef struct { uint64_t s; } or_rng;
+void or_rng_init(or_rng *r, uint64_t seed);
+uint64_t or_rng_next(or_rng *r);
+float or_rng_f32(or_rng *r);
+float or_rng_sym(or_rng *r);
+
+/* ---- quant formats ------------------------------------------------------ */
+size_t or_block_size(int ty);
+size_t or_block_bytes(int ty);
+size_t or_row_bytes(int ty, size_t n);
+int or_act_format(int ty);
+void or_dequantize_row(int ty, const uint8_t *src, float *dst, size_t n);
+void or_quantize_q8_0(const float *x, or_block_q8_0 *out, size_t nblocks);        /* AVX2 avx2.rs:153-184 */
+void or_quantize_q8_0_scalar(const float *x, or_block_q8_0 *out, size_t nblocks); /* quant/mod.rs:175-189 */
+void or_quantize_q8_k(const float *x, or_block_q8k *out, size_t nblocks);         /* quant/mod.rs:191-218 */
+/* quantize::q4_0 / q8_0, quant/mod.rs:265-298 (writes row bytes) */
+void or_quantize_weights_q4_0(const float *x, size_t n, uint8_t *out);
+void or_quantize_weights_q8_0(const float *x, size_t n, uint8_t *out);
+
+/* vec_dot dispatch as selected on an AVX2+FMA+F16C host, kernels/mod.rs:136-232.
+ * act points to float[n], or_block_q8_0[n/32] or or_block_q8k[n/256]. */
+float or_vec_dot(int ty, const uint8_t *w, const void *act, size_t n);
+/* Per-block (Q4_0/Q8_0: per 32; K-quants: per 256) integer dot products. */
+void or_block_idots(int ty, const uint8_t *w, const void *act, size_t n, int32_t *out);
+
+/* float kernels, avx2.rs:186-241 */
+float or_dot_f32(const float *a, const float *b, size_t n);
+float or_dot_f16_f32(const uint16_t *a, const float *b, size_t n);
+void or_axpy_f16(float *y, float alpha, const uint16_t *x, size_t n);
+
+/* ---- ops.rs ------------------------------------------------------------- */
+void or_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps);
+void or_rmsnorm_inplace(float *x, const float *w, size_t n, float eps);
+float or_silu(float x);
+void or_softmax(float *x, size_t n);
+void or_rope_inv_freq(size_t dim, float base, float freq_scale, const float *factors, size_t nfac, float *inv_freq);
+void or_rope_table(const float *inv_freq, size_t half, size_t pos, float *cos_out, float *sin_out);
+void or_rope_apply(float *x, size_t dim, int neox, const float *cos_t, const float *sin_t);
+
+/* ---- turbo.rs ----------------------------------------------------------- */
+#define OR_TURBO_KV_SEED 0x75426F5175616E74ULL
+size_t or_turbo_block_size(size_t d);
+size_t or_turbo_row_bytes(size_t d);
+void or_turbo_signs(size_t d, uint64_t seed, float *signs);
+void or_fwht(float *x, size_t n);
+void or_turbo_rotate(float *x, size_t d, uint64_t seed);
+void or_turbo_rotate_inverse(float *x, size_t d, uint64_t seed);
+void or_turbo_quantize_rotated(const float *y, size_t d, uint8_t *out);
+void or_turbo_quantize(const float *x, size_t d, uint64_t seed, uint8_t *out);
+float or_turbo_dot(const or_block_q8_0 *q, size_t d, const uint8_t *row);
+void or_turbo_axpy(float *y_rot, size_t d, float a, const uint8_t *row);
+void or_turbo_dequantize(const uint8_t *row, size_t d, uint64_t seed, float *out);
+
+/* ---- synthetic GGUF, testing.rs ------------------------------------------ */
+typedef struct {
+    char arch[32];
+    uint32_t n_vocab, n_embd, n_layer, n_head, n_head_kv, head_dim, n_ff, rope_dim, ctx;
+    int32_t wtype, embd_type;
+    int32_t tied_output, qkv_bias, qk_norm, post_norms, fused;
+    uint32_t swa_window, n_expert, n_expert_used, n_ff_exp, n_ff_shexp;
+    int32_t chat_template; /* 0 none, 1 chatml, 2 llama3 */
+    uint64_t seed;
+} or_synth_spec;
+
+int or_synth_tiny(const char *arch, int wtype, or_synth_spec *out);
+int or_synth_preset(const char *name, int wtype, or_synth_spec *out);
+/* Builds the GGUF image; returns its size and sets *out (free with or_free). */
+size_t or_synth_build(const or_synth_spec *spec, uint8_t **out);
+void or_random_weight(or_rng *r, int ty, size_t rows, size_t cols, float gain, uint8_t *out);
+void or_free(void *p);
+
+/* ---- model / backend / engine ------------------------------------------- */
+typedef struct or_model or_model;
+typedef struct or_backend or_backend;
+
+or_model *or_model_load(const uint8_t *gguf, size_t len, char *err, size_t err_len);
+void or_model_free(or_model *m);
+/* flat view of the hyper-parameters: see model.c or_model_config */
+void or_model_config(const or_model *m, int64_t *out, size_t n);
+
+or_backend *or_backend_new(or_model *m, size_t n_ctx, size_t max_batch, int kv_type, int n_threads);
+void or_backend_free(or_backend *b);
+int or_backend_kv_type(const or_backend *b);
+size_t or_backend_kv_bytes(const or_backend *b);
+/* returns 0 or a negative error code (-5 = Runtime), message in err */
+int or_forward(or_backend *b, const uint32_t *tokens, size_t n, size_t pos, int all_logits,
+               float *logits, size_t logits_len, char *err, size_t err_len);
+/* Final normalized hidden rows of the last forward (Backend::hidden). */
+const float *or_hidden(const or_backend *b, size_t *rows);
+/* Raw KV cache bytes of one layer (k or v), [kv_head][slot][row bytes]. */
+const uint8_t *or_kv_layer(const or_backend *b, size_t layer, int which, size_t *bytes);
+/* Capture of intermediate f32 tensors of the last forward (layer il): 0 x after
+ * attention residual, 1 x after ffn residual, 2 attention output (pre-wo), 3 q
+ * after head prep, 4 k after head prep, 5 v, 6 glu output. NULL if not captured. */
+void or_set_capture(or_backend *b, int on);
+const float *or_capture(const or_backend *b, size_t layer, int what, size_t *len);
+
+/* Engine (engine.rs): greedy generation after a prompt, with top-2 margins. */
+uint32_t or_argmax(const float *x, size_t n);
+int or_greedy(or_backend *b, const uint32_t *prompt, size_t n_prompt, size_t n_batch, size_t n_gen,
+              uint32_t *out_tokens, float *out_margin, float *out_logits_first, char *err, size_t err_len);
+/* Engine::bench, engine.rs:540-564: returns pp tok/s and tg tok/s. */
+int or_bench(or_backend *b, size_t n_prompt, size_t n_gen, double *pp_tps, double *tg_tps, char *err, size_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

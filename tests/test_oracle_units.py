@@ -1,0 +1,372 @@
+"""Pins the oracle's unit functions against what the mathematics or an
+independent implementation fixes: IEEE f16 rounding (numpy), hand-built known
+answers for the quantizers, exact integer identities for the block dots, the
+reference's own kernel tests (crates/rie-core/tests/kernels.rs) and the
+TurboQuant invariants of turbo.rs:478-573.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import ggml_np as G
+
+ALL_TYPES = [0, 1, 30, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14]
+BLOCK_TYPES = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14]
+
+
+# ---- f16 ------------------------------------------------------------------------
+def test_f32_to_f16_is_ieee_round_to_nearest_even(oracle):
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 4000).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, 65504.0, 65520.0, 65519.99, 1e-8, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                  2.0 ** -14, 2.0 ** -15 * 1.5, np.inf, -np.inf, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11], np.float32),
+    ]).astype(np.float32)
+    # exact ties in the normal range: mantissa ending in 1 followed by 12 zero bits
+    ties = (np.arange(1, 200, dtype=np.uint32) << 13 | 0x1000 | 0x3F800000).view(np.float32)
+    vals = np.concatenate([vals, ties, -ties])
+    got = np.array([oracle.f32_to_f16(float(v)) for v in vals], np.uint16)
+    want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f16_to_f32_exact_for_every_half(oracle):
+    L = oracle.lib()
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([L.or_f16_to_f32(int(v)) for v in h], np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+
+
+# ---- Rng and random_weight (testing.rs:10-91) ------------------------------------
+def _xorshift_py(seed, n):
+    M = (1 << 64) - 1
+    s = ((seed * 0x9E3779B97F4A7C15) & M) | 1
+    out = []
+    for _ in range(n):
+        s ^= (s << 13) & M
+        s ^= s >> 7
+        s ^= (s << 17) & M
+        out.append(s)
+    return out
+
+
+def test_rng_is_xorshift64_13_7_17(oracle):
+    for seed in (0, 1, 7, 42, 0xDEADBEEF):
+        r = oracle.Rng(seed)
+        assert [r.next_u64() for _ in range(64)] == _xorshift_py(seed, 64)
+
+
+def test_random_weight_layout_and_scales(oracle):
+    """Block bytes are the little-endian Rng stream; scale fields are f16 in
+    [k/2, k] with ~30% negative for signed formats (testing.rs:46-91)."""
+    for ty, k, off in [(2, 0.01, [0]), (8, 0.001, [0]), (12, 0.001, [0, 2]), (14, 0.0001, [208])]:
+        r = oracle.Rng(5)
+        rows, cols = 64, 512
+        w = r.random_weight(ty, rows, cols)
+        bs, bb = G.BLOCK[ty]
+        blocks = w.reshape(-1, bb)
+        stream = np.array(_xorshift_py(5, (blocks.size + 7) // 8), np.uint64).view(np.uint8)[: blocks.size].reshape(-1, bb)
+        mask = np.ones(bb, bool)
+        for o in off:
+            mask[o:o + 2] = False
+        assert np.array_equal(blocks[:, mask], stream[:, mask])
+        for i, o in enumerate(off):
+            s = blocks[:, o:o + 2].copy().view(np.float16).astype(np.float32).reshape(-1)
+            a = np.abs(s)
+            assert a.min() >= np.float32(k * 0.5) * 0.999 and a.max() <= np.float32(k) * 1.001
+            if i == 0 and ty in (2, 8, 14):
+                frac = float((s < 0).mean())
+                assert 0.2 < frac < 0.4
+            else:
+                assert (s > 0).all()
+
+
+# ---- dequantization ---------------------------------------------------------------
+@pytest.mark.parametrize("ty", ALL_TYPES)
+def test_dequantize_matches_independent_numpy(oracle, ty):
+    r = oracle.Rng(3)
+    n = 1024
+    w = r.random_weight(ty, 4, n)
+    got = oracle.dequantize_row(ty, w, 4 * n)
+    want = G.dequantize(ty, w, 4 * n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), ty
+
+
+def test_q4_0_known_block(oracle):
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)  # d = 1.0
+    blk[2:18] = np.arange(16, dtype=np.uint8) | (np.arange(15, -1, -1, dtype=np.uint8) << 4)
+    y = oracle.dequantize_row(2, blk, 32)
+    assert list(y[:16]) == [float(i - 8) for i in range(16)]
+    assert list(y[16:]) == [float(15 - i - 8) for i in range(16)]
+
+
+# ---- activation quantizers ---------------------------------------------------------------
+def test_q8_0_known_answers(oracle):
+    x = np.zeros(64, np.float32)
+    x[32:] = [127.0, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -127.0] + [0.0] * 24  # d = 1, id = 1: exact ties
+    q = oracle.quantize_q8_0(x)
+    assert q[0]["d"] == 0 and q[0]["s"] == 0 and not q[0]["qs"].any()
+    assert list(q[1]["qs"][:8]) == [127, 2, 4, -2, 0, 0, 2, -127]  # round half to even (AVX2)
+    assert q[1]["d"] == np.float32(1.0) and q[1]["s"] == np.float32(6.0)
+    qs = oracle.quantize_q8_0(x, scalar=True)  # RIE_DISABLE=simd: round half away from zero
+    assert list(qs[1]["qs"][:8]) == [127, 3, 4, -3, 1, -1, 2, -127]
+
+
+def test_q8_0_matches_numpy_restatement(oracle):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(32 * 500) * rng.uniform(0.01, 50, 32 * 500)).astype(np.float32)
+    x[:32] = 0
+    q = oracle.quantize_q8_0(x)
+    qs, d, s = G.quantize_q8_0_avx2(x)
+    assert np.array_equal(q["qs"], qs) and np.array_equal(q["d"], d) and np.array_equal(q["s"], s)
+    q = oracle.quantize_q8_0(x, scalar=True)
+    qs, d, s = G.quantize_q8_0_scalar(x)
+    assert np.array_equal(q["qs"], qs) and np.array_equal(q["d"], d) and np.array_equal(q["s"], s)
+
+
+def test_q8_k_known_answers(oracle):
+    x = np.zeros(768, np.float32)
+    x[256 + 3], x[256 + 10] = -2.0, 2.0  # first strictly-largest |x| is negative → d > 0
+    x[512 + 1], x[512 + 9] = 2.0, -2.0   # first is positive → d < 0
+    x[512 + 20] = 0.5
+    q = oracle.quantize_q8_k(x)
+    assert q[0]["d"] == 0 and not q[0]["qs"].any() and not q[0]["bsums"].any()
+    assert q[1]["d"] == np.float32(1.0) / np.float32(63.5)
+    assert q[1]["qs"][3] == -127 and q[1]["qs"][10] == 127
+    assert q[2]["d"] == np.float32(1.0) / np.float32(-63.5)
+    assert q[2]["qs"][1] == -127 and q[2]["qs"][9] == 127
+    assert q[2]["qs"][20] == -32  # -63.5*0.5 = -31.75 → -32
+    assert q[2]["bsums"][0] == -127 + 127 and q[2]["bsums"][1] == -32
+
+
+def test_q8_k_matches_numpy_restatement(oracle):
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(256 * 100) * 3).astype(np.float32)
+    q = oracle.quantize_q8_k(x)
+    qs, bsums, d = G.quantize_q8_k(x)
+    assert np.array_equal(q["qs"], qs) and np.array_equal(q["bsums"], bsums) and np.array_equal(q["d"], d)
+
+
+# ---- int8 block dots ------------------------------------------------------------------------
+def _reference_dot(oracle, ty, w, x):
+    """tests/kernels.rs:10-29: dequantized weights · the quantized activation, in f64"""
+    n = x.size
+    wf = G.dequantize(ty, w, n).astype(np.float64)
+    xa = G.dequant_act(ty, x).astype(np.float64)
+    return float(wf @ xa), float(np.abs(wf * x.astype(np.float64)).sum())
+
+
+@pytest.mark.parametrize("ty", ALL_TYPES)
+def test_vec_dot_matches_dequantized_reference(oracle, ty):
+    """tests/kernels.rs:36-64 with the reference's tolerance 1e-4·Σ|w·x| + 1e-5"""
+    r = oracle.Rng(7)
+    for n in (256, 512, 768, 2048):
+        for _ in range(4):
+            w = r.random_weight(ty, 1, n)
+            x = (np.random.default_rng(n).uniform(-1, 1, n) * 2).astype(np.float32)
+            act = oracle.quantize_act(ty, x)
+            got = oracle.vec_dot(ty, w, act, n)
+            want, mag = _reference_dot(oracle, ty, w, x)
+            assert abs(got - want) <= 1e-4 * mag + 1e-5, (ty, n, got, want)
+
+
+@pytest.mark.parametrize("ty", [2, 8, 6])
+def test_block_idots_are_exact_integer_dots(oracle, ty):
+    """For symmetric formats w_j = d_w·c_j exactly, so Σ_j w_j·q_j = d_w·idot in f64."""
+    r = oracle.Rng(11)
+    n = 2048
+    w = r.random_weight(ty, 1, n)
+    x = np.random.default_rng(3).standard_normal(n).astype(np.float32)
+    act = oracle.quantize_q8_0(x)
+    idots = oracle.block_idots(ty, w, act, n)
+    wf = G.dequantize(ty, w, n).astype(np.float64).reshape(-1, 32)
+    bs, bb = G.BLOCK[ty]
+    d = w.reshape(-1, bb)[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1)
+    lhs = (wf * act["qs"].astype(np.float64)).sum(axis=1)
+    assert np.array_equal(lhs, d * idots.astype(np.float64))
+
+
+@pytest.mark.parametrize("ty", [12, 13, 14])
+def test_kquant_block_idots_decomposition(oracle, ty):
+    """d·sumi − dmin·summ reproduces Σ dequant(w)·q to float precision; a wrong
+    sub-block index or scale would miss by O(1)."""
+    r = oracle.Rng(13)
+    n = 2048
+    w = r.random_weight(ty, 1, n)
+    x = np.random.default_rng(4).standard_normal(n).astype(np.float32)
+    act = oracle.quantize_q8_k(x)
+    ints = oracle.block_idots(ty, w, act, n).reshape(-1, 2).astype(np.float64)
+    bb = G.BLOCK[ty][1]
+    blk = w.reshape(-1, bb)
+    if ty == 14:
+        d = blk[:, 208:210].copy().view(np.float16).astype(np.float64).reshape(-1)
+        approx = d * ints[:, 0]
+    else:
+        d = blk[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1)
+        dm = blk[:, 2:4].copy().view(np.float16).astype(np.float64).reshape(-1)
+        approx = d * ints[:, 0] - dm * ints[:, 1]
+    wf = G.dequantize(ty, w, n).astype(np.float64).reshape(-1, 256)
+    exact = (wf * act["qs"].astype(np.float64)).sum(axis=1)
+    assert np.allclose(approx, exact, rtol=1e-5, atol=1e-6 * np.abs(wf).sum(axis=1).max())
+
+
+def test_float_kernels(oracle):
+    """tests/kernels.rs:120-142"""
+    L = oracle.lib()
+    rng = np.random.default_rng(5)
+    for n in (1, 7, 8, 15, 16, 33, 128, 1000):
+        a = rng.uniform(-1, 1, n).astype(np.float32)
+        b = rng.uniform(-1, 1, n).astype(np.float32)
+        assert abs(L.or_dot_f32(oracle.ptr(a), oracle.ptr(b), n) - float(a.astype(np.float64) @ b)) < 1e-4 * n
+        h = a.astype(np.float16)
+        hb = np.ascontiguousarray(h.view(np.uint16))
+        ah = h.astype(np.float64)
+        assert abs(L.or_dot_f16_f32(oracle.ptr(hb), oracle.ptr(b), n) - float(ah @ b)) < 1e-4 * n
+        y = b.copy()
+        L.or_axpy_f16(oracle.ptr(y), 0.5, oracle.ptr(hb), n)
+        assert np.abs(y - (b + 0.5 * ah)).max() < 1e-5
+
+
+# ---- ops -------------------------------------------------------------------------------------
+def test_rope_matches_complex_rotation(oracle):
+    """ops.rs:115-130"""
+    import ctypes as C
+    L = oracle.lib()
+    inv = np.zeros(4, np.float32)
+    L.or_rope_inv_freq(8, 10000.0, 1.0, None, 0, oracle.ptr(inv))
+    want = np.float32(10000.0) ** (np.float32(-2.0) * np.arange(4, dtype=np.float32) / np.float32(8))
+    assert np.allclose(inv, want, rtol=2e-7)
+    c, s = np.zeros(4, np.float32), np.zeros(4, np.float32)
+    L.or_rope_table(oracle.ptr(inv), 4, 5, oracle.ptr(c), oracle.ptr(s))
+    x0 = (np.arange(8, dtype=np.float32) * np.float32(0.3) - 1).astype(np.float32)
+    x = x0.copy()
+    L.or_rope_apply(oracle.ptr(x), 8, 0, oracle.ptr(c), oracle.ptr(s))
+    assert abs((x0 ** 2).sum() - (x ** 2).sum()) < 1e-4
+    assert abs(x[0] - (x0[0] * math.cos(5) - x0[1] * math.sin(5))) < 1e-5
+    # NEOX pairs (i, i+d/2)
+    y = x0.copy()
+    L.or_rope_apply(oracle.ptr(y), 8, 1, oracle.ptr(c), oracle.ptr(s))
+    z = (x0[:4] + 1j * x0[4:]) * np.exp(1j * 5.0 * inv.astype(np.float64))
+    assert np.allclose(y[:4], z.real, atol=1e-5) and np.allclose(y[4:], z.imag, atol=1e-5)
+
+
+def test_softmax_sums_to_one(oracle):
+    v = np.array([1.0, 2.0, 3.0, -1000.0], np.float32)
+    oracle.lib().or_softmax(oracle.ptr(v), 4)
+    assert abs(v.sum() - 1) < 1e-6 and v[3] == 0
+
+
+# ---- TurboQuant (turbo.rs) ---------------------------------------------------------------------
+LM4 = [0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6180, 2.0690, 2.7326]
+KV_LEVELS_I8 = [-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126]
+
+
+def test_lloyd_max_levels_and_int8_table():
+    """turbo.rs:493-512: each level is the conditional mean of N(0,1) over its
+    cell; the int8 table is round(46·level) (turbo.rs:126-127)."""
+    c = [-v for v in reversed(LM4)] + LM4
+    phi = lambda t: math.exp(-0.5 * t * t) / math.sqrt(2 * math.pi)
+    for i in range(16):
+        lo = -12.0 if i == 0 else 0.5 * (c[i - 1] + c[i])
+        hi = 12.0 if i == 15 else 0.5 * (c[i] + c[i + 1])
+        xs = np.linspace(lo, hi, 20001)
+        w = np.exp(-0.5 * xs * xs)
+        assert abs((xs * w).sum() / w.sum() - c[i]) < 2e-3
+    assert [int(round(46 * v)) for v in c] == KV_LEVELS_I8
+
+
+def _splitmix_sign(seed, i):
+    M = (1 << 64) - 1
+    z = (seed + i * 0x9E3779B97F4A7C15) & M
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+    return 1.0 if ((z ^ (z >> 31)) & 1) == 0 else -1.0
+
+
+def _hadamard(n):
+    H = np.array([[1.0]])
+    while H.shape[0] < n:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+@pytest.mark.parametrize("d", [64, 96, 128, 80])
+def test_rotation_is_block_hadamard_times_signs(oracle, d):
+    """R = H·D per power-of-two block (turbo.rs:91-118), orthogonal and undone by Rᵀ."""
+    b = oracle.lib().or_turbo_block_size(d)
+    assert b == max(p for p in (1, 2, 4, 8, 16, 32, 64, 128, 256) if d % p == 0)
+    signs = np.array([_splitmix_sign(7, i) for i in range(d)])
+    R = np.zeros((d, d))
+    for o in range(0, d, b):
+        R[o:o + b, o:o + b] = _hadamard(b) / math.sqrt(b)
+    R = R @ np.diag(signs)
+    x = np.random.default_rng(d).uniform(-0.5, 0.5, d).astype(np.float32)
+    y = oracle.turbo_rotate(x, seed=7)
+    assert np.allclose(y, R @ x, atol=1e-6)
+    assert np.allclose(oracle.turbo_rotate(y, seed=7, inverse=True), x, atol=1e-5)
+
+
+def _turbo_quantize_rotated_np(y):
+    """turbo.rs:140-164 for one 128-block, with sequential float32 sums"""
+    c = (np.array(KV_LEVELS_I8, np.float32) / np.float32(46.0)).astype(np.float32)
+    mids = (np.float32(0.5) * (c[:-1] + c[1:])).astype(np.float32)
+    sq = np.cumsum((y * y).astype(np.float32), dtype=np.float32)[-1]
+    rms = np.sqrt(np.float32(sq / np.float32(y.size)), dtype=np.float32)
+    inv = np.float32(1.0) / rms if rms > 0 else np.float32(0.0)
+    q = (((y * inv).astype(np.float32))[:, None] > mids[None, :]).sum(axis=1)
+    num = np.cumsum((y * c[q]).astype(np.float32), dtype=np.float32)[-1]
+    den = np.cumsum((c[q] * c[q]).astype(np.float32), dtype=np.float32)[-1]
+    s = np.float32(num / den) if den > 0 else np.float32(0)
+    codes = np.zeros(y.size // 2, np.uint8)
+    for g in range(y.size):
+        codes[(g // 32) * 16 + g % 16] |= np.uint8(q[g] << ((g % 32) // 16 * 4))
+    return np.concatenate([np.array([s], np.float16).view(np.uint8), codes])
+
+
+def test_turbo_codes_match_numpy_restatement(oracle):
+    rng = np.random.default_rng(9)
+    for _ in range(50):
+        x = rng.standard_normal(128).astype(np.float32) * np.float32(rng.uniform(0.01, 10))
+        y = oracle.turbo_rotate(x)
+        row = oracle.turbo_quantize(x)
+        assert np.array_equal(row, _turbo_quantize_rotated_np(y))
+
+
+def test_four_bit_rows_accurate_with_outliers_and_dot_identities(oracle):
+    """turbo.rs:532-573"""
+    d = 128
+    assert oracle.turbo_row_bytes(128) == 66 and oracle.turbo_row_bytes(96) == 54
+    rng = np.random.default_rng(3)
+    rel = 0.0
+    L = oracle.lib()
+    for _ in range(50):
+        x = (rng.uniform(0, 1, d) - 0.5).astype(np.float32)
+        x[5], x[77] = 20.0, -9.0
+        row = oracle.turbo_quantize(x)
+        y = oracle.turbo_dequantize(row, d)
+        rel += math.sqrt(float(((x - y) ** 2).sum() / (x ** 2).sum()))
+        q = (rng.uniform(0, 1, d) - 0.5).astype(np.float32)
+        direct = float(q.astype(np.float64) @ y)
+        qr = oracle.turbo_rotate(q)
+        qq = oracle.quantize_q8_0(qr)
+        deq = (qq["qs"].astype(np.float32) * qq["d"][:, None]).reshape(-1)
+        yr = np.zeros(d, np.float32)
+        L.or_turbo_axpy(oracle.ptr(yr), d, 1.0, oracle.ptr(row))
+        exact = float(deq.astype(np.float64) @ yr)
+        got = L.or_turbo_dot(oracle.ptr(qq), d, oracle.ptr(row))
+        assert abs(got - exact) < 1e-3 * (1 + abs(exact))
+        assert abs(exact - direct) < 0.01 * np.linalg.norm(q) * np.linalg.norm(y)
+    assert rel / 50 < 0.12
+
+
+def test_quantize_weights_roundtrip(oracle):
+    """tests/kernels.rs:107-118"""
+    x = np.random.default_rng(3).uniform(-1, 1, 1024).astype(np.float32)
+    for ty, tol in ((8, 0.01), (2, 0.15)):
+        y = G.dequantize(ty, oracle.quantize_weights(ty, x), 1024)
+        assert np.abs(y - x).max() <= tol * np.abs(x).max()
