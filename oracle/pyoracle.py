@@ -221,7 +221,7 @@ def synth_build(spec: SynthSpec) -> bytes:
     p = C.POINTER(C.c_uint8)()
     n = lib().or_synth_build(C.byref(spec), C.byref(p))
     try:
-        return C.string_at(p, n)
+        return np.ctypeslib.as_array(p, (n,)).tobytes()  # string_at takes a 32-bit size
     finally:
         lib().or_free(p)
 

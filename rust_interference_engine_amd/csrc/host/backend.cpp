@@ -1,0 +1,638 @@
+// backend.cpp — HipBackend: the per-token forward loop of RIE
+// (CpuBackend::forward_impl, model/cpu.rs:210-409 in the reference) on one
+// MI355X.  The GGUF tensor data is uploaded once, unchanged, into one HBM
+// buffer; every weight is a view into it.  A forward call is a fixed sequence
+// of stream-ordered kernel launches; the single-token decode step is captured
+// once in a HIP graph whose only per-step inputs live in device memory
+// ({pos} and the token id), so greedy decoding never returns to the host.
+#include "backend.hpp"
+
+#include "../kernels.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace rie {
+
+static Error rt_err(const std::string &m) { return Error{E_RUNTIME, m}; }
+
+template <class T>
+static T *dalloc(std::vector<void *> &list, size_t count) {
+    void *p = nullptr;
+    size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    RIE_HIP_CHECK(hipMalloc(&p, bytes));
+    RIE_HIP_CHECK(hipMemset(p, 0, bytes));
+    list.push_back(p);
+    return (T *)p;
+}
+
+static bool gemv_type_ok(int ty, size_t K) { return gemv_supported(ty, K); }
+
+HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg) {
+    Gguf g = Gguf::parse(gguf, len);
+    m_ = HostModel::load(g);
+    const ModelConfig &c = m_.cfg;
+    n_ctx_ = std::max<size_t>(cfg.n_ctx, 1);
+    max_batch_ = std::min(std::max<size_t>(cfg.max_batch, 1), n_ctx_);
+    use_graph_ = cfg.use_graph;
+    device_ = cfg.device;
+    int kv = cfg.kv_type;
+    // cpu.rs:103-108: Q8_0 needs hd%32==0, Turbo4 needs hd%32==0 and hd<=512
+    if (kv == 1 && c.head_dim % 32 != 0) kv = 0;
+    if (kv == 2 && (c.head_dim % 32 != 0 || c.head_dim > 512)) kv = 0;
+    kv_type_ = kv;
+    if (c.head_dim > 256) throw Error{E_UNSUPPORTED, "unsupported: head dim " + std::to_string(c.head_dim) + " on the HIP backend"};
+    if (c.n_head / c.n_head_kv > 8) throw Error{E_UNSUPPORTED, "unsupported: more than 8 query heads per KV head"};
+
+    // shape/type checks: every matrix needs a kernel
+    auto need = [&](const HostWeight &w, const char *what) {
+        if (!w.present()) return;
+        if (!gemv_type_ok(w.ty, w.cols))
+            throw Error{E_UNSUPPORTED, std::string("unsupported: ") + what + " of type " + type_name(w.ty) + " with " +
+                                           std::to_string(w.cols) + " columns on the HIP backend"};
+    };
+    for (auto &L : m_.layers) {
+        need(L.wq, "attn_q"); need(L.wk, "attn_k"); need(L.wv, "attn_v"); need(L.wo, "attn_output");
+        need(L.gate, "ffn_gate"); need(L.up, "ffn_up"); need(L.down, "ffn_down"); need(L.router, "ffn_gate_inp");
+        if (L.moe && L.shexp_gate.present()) throw Error{E_UNSUPPORTED, "unsupported: shared experts on the HIP backend"};
+        for (const HostWeight *nw : {&L.attn_norm, &L.ffn_norm, &L.q_norm, &L.k_norm, &L.bq, &L.bk, &L.bv, &L.post_attn_norm, &L.post_ffn_norm})
+            if (nw->present() && nw->ty != T_F32) throw Error{E_UNSUPPORTED, "unsupported: non-F32 norm/bias vectors"};
+    }
+    need(m_.output, "output");
+    {
+        int et = m_.token_embd.ty;
+        if (!(et == T_F32 || et == T_F16 || et == T_Q4_0 || et == T_Q8_0 || et == T_Q4_K || et == T_Q6_K))
+            throw Error{E_UNSUPPORTED, std::string("unsupported: token_embd of type ") + type_name(et)};
+    }
+
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    RIE_HIP_CHECK(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
+    hipDeviceProp_t prop;
+    RIE_HIP_CHECK(hipGetDeviceProperties(&prop, device_));
+    name_ = std::string("HIP ") + prop.gcnArchName + " (" + std::to_string(prop.multiProcessorCount) + " CUs)";
+
+    // ---- weights: the GGUF data region, once, unchanged ----
+    blob_base_off_ = g.data_start;
+    blob_len_ = len - g.data_start;
+    RIE_HIP_CHECK(hipMalloc(&d_blob_, blob_len_ + 4096));  // slack for realigning vector loads at the end
+    RIE_HIP_CHECK(hipMemcpy(d_blob_, gguf + g.data_start, blob_len_, hipMemcpyHostToDevice));
+    RIE_HIP_CHECK(hipMemset(d_blob_ + blob_len_, 0, 4096));
+
+    const size_t hd = c.head_dim, E = c.n_embd, qd = c.q_dim(), kvd = c.kv_dim();
+    embd_ = dev(m_.token_embd);
+    out_w_ = dev(m_.output.rows > c.n_vocab ? m_.output.slice_rows(0, c.n_vocab) : m_.output);
+    out_norm_ = dev_vec(m_.output_norm);
+    ff_max_ = 0;
+    for (auto &L : m_.layers) {
+        DevLayer D{};
+        D.attn_norm = dev_vec(L.attn_norm);
+        D.ffn_norm = dev_vec(L.ffn_norm);
+        D.q_norm = dev_vec(L.q_norm);
+        D.k_norm = dev_vec(L.k_norm);
+        D.bq = dev_vec(L.bq);
+        D.bk = dev_vec(L.bk);
+        D.bv = dev_vec(L.bv);
+        D.post_attn_norm = dev_vec(L.post_attn_norm);
+        D.post_ffn_norm = dev_vec(L.post_ffn_norm);
+        D.wq = dev(L.wq); D.wk = dev(L.wk); D.wv = dev(L.wv); D.wo = dev(L.wo);
+        D.gate = dev(L.gate); D.up = dev(L.up); D.down = dev(L.down);
+        D.moe = L.moe;
+        if (L.moe) {
+            D.router = dev(L.router);
+            D.n_used = L.n_used;
+            D.ff = c.n_ff_exp;
+            D.norm_topk = L.norm_topk;
+            D.unit_weights = L.unit_weights;
+        } else {
+            D.ff = L.gate.rows;
+        }
+        ff_max_ = std::max(ff_max_, D.ff);
+        layers_.push_back(D);
+    }
+
+    // ---- KV cache: [layer][kv_head][slot][row] ----
+    const size_t rb = kv_row_bytes();
+    for (size_t il = 0; il < c.n_layer; il++) {
+        DevLayer &D = layers_[il];
+        D.slots = c.is_swa(il) ? std::min(c.swa_window + max_batch_, n_ctx_) : n_ctx_;
+        const size_t rows = c.n_head_kv * D.slots;
+        D.k_cache = dalloc<uint8_t>(allocs_, rows * rb);
+        D.v_cache = dalloc<uint8_t>(allocs_, rows * rb);
+        kv_bytes_ += 2 * rows * rb;
+        if (kv_type_ == 2) {  // one f16 scale per rotation block (turbo.rs:133-138)
+            D.k_scale = dalloc<uint16_t>(allocs_, rows * turbo_blocks());
+            D.v_scale = dalloc<uint16_t>(allocs_, rows * turbo_blocks());
+            kv_bytes_ += 4 * rows * turbo_blocks();
+        }
+    }
+
+    // ---- RoPE tables from libm powf/sinf/cosf, as ops.rs:65-89 computes them ----
+    {
+        const size_t half = c.rope_dim / 2;
+        auto table = [&](float base, float fscale, bool factors, float *&dc, float *&ds) {
+            std::vector<float> inv(std::max<size_t>(half, 1));
+            std::vector<float> fac;
+            if (factors && m_.rope_factors.present()) {
+                fac.resize(m_.rope_factors.rows * m_.rope_factors.cols);
+                std::memcpy(fac.data(), gguf + m_.rope_factors.off, fac.size() * 4);
+            }
+            for (size_t i = 0; i < half; i++) {
+                float f = powf(base, -2.0f * (float)i / (float)c.rope_dim) * fscale;
+                if (i < fac.size() && fac[i] != 0.0f) f /= fac[i];
+                inv[i] = f;
+            }
+            std::vector<float> cs(n_ctx_ * std::max<size_t>(half, 1)), sn(cs.size());
+            for (size_t p = 0; p < n_ctx_; p++)
+                for (size_t i = 0; i < half; i++) {
+                    const float th = (float)p * inv[i];
+                    sn[p * half + i] = sinf(th);
+                    cs[p * half + i] = cosf(th);
+                }
+            dc = dalloc<float>(allocs_, cs.size());
+            ds = dalloc<float>(allocs_, sn.size());
+            RIE_HIP_CHECK(hipMemcpy(dc, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+            RIE_HIP_CHECK(hipMemcpy(ds, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+        };
+        table(c.rope_base, c.rope_freq_scale, true, d_cos_, d_sin_);
+        if (c.has_rope_swa) table(c.rope_base_swa, 1.0f, false, d_cos_swa_, d_sin_swa_);
+    }
+    // TurboQuant sign pattern (turbo.rs:78-89) for KV_SEED
+    {
+        std::vector<float> s(hd);
+        const uint64_t seed = 0x75426F5175616E74ULL;
+        for (size_t i = 0; i < hd; i++) {
+            uint64_t z = seed + (uint64_t)i * 0x9E3779B97F4A7C15ULL;
+            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+            z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+            s[i] = ((z ^ (z >> 31)) & 1u) == 0 ? 1.0f : -1.0f;
+        }
+        d_signs_ = dalloc<float>(allocs_, hd);
+        RIE_HIP_CHECK(hipMemcpy(d_signs_, s.data(), hd * 4, hipMemcpyHostToDevice));
+    }
+
+    // ---- scratch ----
+    const size_t mb = max_batch_;
+    kmax_ = std::max({E, qd, ff_max_});
+    d_tokens_ = dalloc<uint32_t>(allocs_, mb);
+    d_next_ = dalloc<uint32_t>(allocs_, 1);
+    d_gen_ = dalloc<uint32_t>(allocs_, std::max<size_t>(n_ctx_, 1));
+    d_pos_ = dalloc<int>(allocs_, 4);
+    d_x_ = dalloc<float>(allocs_, mb * E);
+    d_xn_ = dalloc<float>(allocs_, mb * kmax_);
+    d_q_ = dalloc<float>(allocs_, mb * qd);
+    d_k_ = dalloc<float>(allocs_, mb * kvd);
+    d_v_ = dalloc<float>(allocs_, mb * kvd);
+    d_kcap_ = dalloc<float>(allocs_, mb * kvd);
+    d_att_ = dalloc<float>(allocs_, mb * qd);
+    d_o_ = dalloc<float>(allocs_, mb * E);
+    d_h_ = dalloc<float>(allocs_, mb * ff_max_ * (c.n_expert ? c.n_expert_used : 1));
+    d_logits_ = dalloc<float>(allocs_, mb * c.n_vocab);
+    const size_t kq = mb * kmax_ * (c.n_expert ? c.n_expert_used : 1);
+    act0_.qs = dalloc<int8_t>(allocs_, kq);
+    act0_.d = dalloc<float>(allocs_, kq / 32);
+    act0_.s = dalloc<float>(allocs_, kq / 32);
+    act0_.isum = dalloc<int32_t>(allocs_, kq / 32);
+    actk_.qs = dalloc<int8_t>(allocs_, kq);
+    actk_.d = dalloc<float>(allocs_, kq / 256 + 1);
+    actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
+    part_floats_ = (size_t)32 * mb * c.n_head * (hd + 2);
+    d_part_ = dalloc<float>(allocs_, part_floats_);
+    d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
+    d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
+    if (c.n_expert) {
+        d_router_ = dalloc<float>(allocs_, mb * c.n_expert);
+        d_moe_w_ = dalloc<float>(allocs_, mb * c.n_expert_used);
+        d_moe_sel_ = dalloc<int>(allocs_, mb * c.n_expert_used);
+    }
+    cap_.resize(7);
+    RIE_HIP_CHECK(hipDeviceSynchronize());
+}
+
+HipBackend::~HipBackend() {
+    if (st_) (void)hipStreamSynchronize(st_);
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    for (void *p : allocs_) (void)hipFree(p);
+    if (d_blob_) (void)hipFree(d_blob_);
+    if (st_) (void)hipStreamDestroy(st_);
+}
+
+DevWeight HipBackend::dev(const HostWeight &w) const {
+    DevWeight d;
+    if (!w.present()) return d;
+    d.ty = w.ty;
+    d.rows = w.rows;
+    d.cols = w.cols;
+    d.data = d_blob_ + (w.off - blob_base_off_);
+    return d;
+}
+
+const float *HipBackend::dev_vec(const HostWeight &w) {
+    if (!w.present()) return nullptr;
+    return (const float *)(const void *)(d_blob_ + (w.off - blob_base_off_));
+}
+
+size_t HipBackend::kv_row_bytes() const {
+    const size_t hd = m_.cfg.head_dim;
+    if (kv_type_ == 0) return hd * 2;
+    if (kv_type_ == 1) return hd / 32 * 34;
+    return hd / 2;
+}
+
+void HipBackend::check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw rt_err(std::string("HIP launch failed in ") + what + ": " + hipGetErrorString(e));
+}
+
+// QuantActs::prepare (matmul.rs:34-71): quantize x (optionally RMS-normalized)
+// once per activation format the given weights consume.
+void HipBackend::prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32) {
+    bool need[3] = {want_f32, false, false};
+    for (int i = 0; i < nw; i++)
+        if (ws[i] && ws[i]->ty >= 0) need[act_format(ws[i]->ty)] = true;
+    const float eps = m_.cfg.rms_eps;
+    bool wrote_f32 = false;
+    if (need[ACT_Q8_0]) {
+        launch_rmsnorm_quant(x, K, norm, eps, n, K, need[ACT_F32] ? d_xn_ : nullptr, ACT_Q8_0, act0_, st_);
+        wrote_f32 = need[ACT_F32];
+    }
+    if (need[ACT_Q8K]) {
+        launch_rmsnorm_quant(x, K, norm, eps, n, K, (need[ACT_F32] && !wrote_f32) ? d_xn_ : nullptr, ACT_Q8K, actk_, st_);
+        wrote_f32 = wrote_f32 || need[ACT_F32];
+    }
+    if (need[ACT_F32] && !wrote_f32) {
+        if (norm) launch_rmsnorm(x, K, norm, eps, n, K, d_xn_, K, 0, st_);
+        else RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, x, (size_t)n * K * 4, hipMemcpyDeviceToDevice, st_));
+    }
+    check_launch("prepare");
+}
+
+// matmul_multi (matmul.rs:136-176): decode-sized batches stream the weights
+// through the GEMV kernels; prompt batches go to the int8 MFMA GEMM.
+void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K) {
+    // group by activation format: each launch reads one activation batch
+    for (int i = 0; i < nseg; i++) {
+        const int fmt = act_format(segs[i].w.ty);
+        const ActQ8 &a = fmt == ACT_Q8K ? actk_ : act0_;
+        bool done = false;
+        if (n > 8 && gemm_supported(segs[i].w.ty, K)) done = launch_gemm(&segs[i], 1, a, n, K, st_);
+        if (!done && !launch_gemv(&segs[i], 1, a, d_xn_, n, K, st_))
+            throw Error{E_UNSUPPORTED, std::string("unsupported: matmul of type ") + type_name(segs[i].w.ty)};
+    }
+    check_launch("matmul");
+}
+
+void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd, ff = (int)L.ff;
+    const DevWeight *ws[2] = {&L.gate, &L.up};
+    prepare(d_x_, L.ffn_norm, n, E, ws, 2, false);
+    mark("rmsnorm_quant");
+    const ActQ8 &a = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
+    bool done = false;
+    if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
+    if (!done && !launch_gemv_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, st_))
+        throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
+    check_launch("ffn glu");
+    mark("matmul_gate_up_glu");
+    const int fmt = act_format(L.down.ty);
+    if (fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_h_, (size_t)n * ff * 4, hipMemcpyDeviceToDevice, st_));
+    else launch_quant_only(d_h_, ff, n, ff, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+    mark("quant");
+    GemvSeg s{L.down, out, E, epi};
+    matmul(&s, 1, n, ff);
+    mark("matmul_down");
+}
+
+void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logits, int n_split) {
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd, qd = (int)c.q_dim(), kvd = (int)c.kv_dim(), hd = (int)c.head_dim;
+    launch_embed(d_tokens_, n, embd_, c.embd_scale, d_x_, st_);
+    check_launch("embed");
+    mark("embed");
+    for (size_t il = 0; il < c.n_layer; il++) {
+        const DevLayer &L = layers_[il];
+        const bool swa = c.is_swa(il);
+        // ---- attention block ----
+        const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
+        prepare(d_x_, L.attn_norm, n, E, ws, 3, false);
+        mark("rmsnorm_quant");
+        GemvSeg qkv[3] = {{L.wq, d_q_, qd, EPI_STORE}, {L.wk, d_k_, kvd, EPI_STORE}, {L.wv, d_v_, kvd, EPI_STORE}};
+        matmul(qkv, 3, n, E);
+        mark("matmul_qkv");
+        if (capture_ && !in_capture_) {
+            RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        }
+        HeadPrepArgs hp{};
+        hp.q = d_q_;
+        hp.k = d_k_;
+        hp.v = d_v_;
+        hp.bq = L.bq; hp.bk = L.bk; hp.bv = L.bv;
+        hp.q_norm = L.q_norm; hp.k_norm = L.k_norm;
+        hp.cos_t = (swa && d_cos_swa_) ? d_cos_swa_ : d_cos_;
+        hp.sin_t = (swa && d_sin_swa_) ? d_sin_swa_ : d_sin_;
+        hp.n_tok = n; hp.pos0 = (int)pos0; hp.n_head = (int)c.n_head; hp.n_kv = (int)c.n_head_kv; hp.hd = hd;
+        hp.rope_dim = (int)c.rope_dim; hp.neox = c.rope_neox;
+        hp.eps = c.rms_eps; hp.attn_scale = c.attn_scale;
+        hp.kv_type = kv_type_;
+        hp.k_cache = L.k_cache; hp.v_cache = L.v_cache; hp.k_scale = L.k_scale; hp.v_scale = L.v_scale;
+        hp.slots = (int)L.slots;
+        hp.d_pos0 = d_pos0;
+        hp.turbo_signs = d_signs_;
+        hp.k_out = (capture_ && !in_capture_) ? d_kcap_ : nullptr;
+        if (capture_ && !in_capture_) {
+            cap_[5].resize(c.n_layer);
+            cap_[5][il].resize((size_t)n * kvd);
+            RIE_HIP_CHECK(hipMemcpy(cap_[5][il].data(), d_v_, (size_t)n * kvd * 4, hipMemcpyDeviceToHost));
+        }
+        launch_head_prep(hp, st_);
+        check_launch("head_prep");
+        mark("head_prep_kv_append");
+        if (capture_ && !in_capture_) {
+            RIE_HIP_CHECK(hipStreamSynchronize(st_));
+            cap_[3].resize(c.n_layer);
+            cap_[3][il].resize((size_t)n * qd);
+            RIE_HIP_CHECK(hipMemcpy(cap_[3][il].data(), d_q_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
+            cap_[4].resize(c.n_layer);
+            cap_[4][il].resize((size_t)n * kvd);
+            RIE_HIP_CHECK(hipMemcpy(cap_[4][il].data(), d_kcap_, (size_t)n * kvd * 4, hipMemcpyDeviceToHost));
+        }
+        AttnArgs aa{};
+        aa.q = d_q_;
+        aa.k_cache = L.k_cache; aa.v_cache = L.v_cache; aa.k_scale = L.k_scale; aa.v_scale = L.v_scale;
+        aa.n_tok = n; aa.pos0 = (int)pos0; aa.n_head = (int)c.n_head; aa.n_kv = (int)c.n_head_kv; aa.hd = hd;
+        aa.slots = (int)L.slots; aa.window = swa ? (int)c.swa_window : 0; aa.kv_type = kv_type_;
+        aa.softcap = c.attn_softcap;
+        aa.part = d_part_;
+        aa.n_split = n_split;
+        aa.att = d_att_;
+        const int wo_fmt = act_format(L.wo.ty);
+        aa.att_fmt = wo_fmt == ACT_Q8_0 ? ACT_Q8_0 : -1;
+        aa.att_q = act0_;
+        aa.d_pos0 = d_pos0;
+        aa.turbo_signs = d_signs_;
+        launch_attention(aa, st_);
+        check_launch("attention");
+        mark("attention");
+        if (capture_ && !in_capture_) {
+            RIE_HIP_CHECK(hipStreamSynchronize(st_));
+            cap_[2].resize(c.n_layer);
+            cap_[2][il].resize((size_t)n * qd);
+            RIE_HIP_CHECK(hipMemcpy(cap_[2][il].data(), d_att_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
+        }
+        if (wo_fmt == ACT_Q8K) launch_quant_only(d_att_, qd, n, qd, ACT_Q8K, actk_, st_);
+        if (wo_fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_att_, (size_t)n * qd * 4, hipMemcpyDeviceToDevice, st_));
+        const bool direct = !L.post_attn_norm && c.residual_scale == 1.0f;
+        GemvSeg so{L.wo, direct ? d_x_ : d_o_, E, direct ? EPI_ADD : EPI_STORE};
+        matmul(&so, 1, n, qd);
+        mark("matmul_wo");
+        if (!direct) {
+            if (L.post_attn_norm) launch_rmsnorm(d_o_, E, L.post_attn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);
+            launch_add_inplace(d_x_, d_o_, (size_t)n * E, c.residual_scale, st_);
+        }
+        if (capture_ && !in_capture_) {
+            RIE_HIP_CHECK(hipStreamSynchronize(st_));
+            cap_[0].resize(c.n_layer);
+            cap_[0][il].resize((size_t)n * E);
+            RIE_HIP_CHECK(hipMemcpy(cap_[0][il].data(), d_x_, (size_t)n * E * 4, hipMemcpyDeviceToHost));
+        }
+        // ---- feed-forward block ----
+        const bool fdirect = !L.post_ffn_norm && c.residual_scale == 1.0f;
+        if (L.moe) {
+            ffn_moe(L, n);
+        } else {
+            ffn_dense(L, n, fdirect ? d_x_ : d_o_, fdirect ? EPI_ADD : EPI_STORE);
+            if (capture_ && !in_capture_) {
+                RIE_HIP_CHECK(hipStreamSynchronize(st_));
+                cap_[6].resize(c.n_layer);
+                cap_[6][il].resize((size_t)n * L.ff);
+                RIE_HIP_CHECK(hipMemcpy(cap_[6][il].data(), d_h_, (size_t)n * L.ff * 4, hipMemcpyDeviceToHost));
+            }
+            if (!fdirect) {
+                if (L.post_ffn_norm) launch_rmsnorm(d_o_, E, L.post_ffn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);
+                launch_add_inplace(d_x_, d_o_, (size_t)n * E, c.residual_scale, st_);
+            }
+        }
+        check_launch("layer");
+        if (capture_ && !in_capture_) {
+            RIE_HIP_CHECK(hipStreamSynchronize(st_));
+            cap_[1].resize(c.n_layer);
+            cap_[1][il].resize((size_t)n * E);
+            RIE_HIP_CHECK(hipMemcpy(cap_[1][il].data(), d_x_, (size_t)n * E * 4, hipMemcpyDeviceToHost));
+        }
+    }
+    const int first = all_logits ? 0 : n - 1;
+    head(first, n - first);
+}
+
+// output head (cpu.rs:388-407): final RMSNorm of the requested rows, logits
+void HipBackend::head(int first, int m) {
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd;
+    const DevWeight *ws[1] = {&out_w_};
+    // the normalized rows are kept in d_xn_ for Backend::hidden
+    const int fmt = act_format(out_w_.ty);
+    const float *xr = d_x_ + (size_t)first * E;
+    if (fmt == ACT_F32) {
+        launch_rmsnorm(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, E, 0, st_);
+    } else {
+        launch_rmsnorm_quant(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+    }
+    (void)ws;
+    mark("rmsnorm_quant");
+    GemvSeg s{out_w_, d_logits_, (int)c.n_vocab, EPI_STORE};
+    matmul(&s, 1, m, E);
+    mark("matmul_output");
+    const size_t total = (size_t)m * c.n_vocab;
+    if (c.logit_scale != 1.0f) launch_scale(d_logits_, total, c.logit_scale, st_);
+    if (c.final_softcap > 0.0f) launch_softcap(d_logits_, total, c.final_softcap, st_);
+    check_launch("head");
+}
+
+void HipBackend::ffn_moe(const DevLayer &L, int n) {
+    (void)L;
+    (void)n;
+    throw Error{E_UNSUPPORTED, "unsupported: mixture-of-experts layers on the HIP backend"};
+}
+
+void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_logits, float *logits, size_t logits_len) {
+    const ModelConfig &c = m_.cfg;
+    hidden_rows_ = 0;
+    if (n == 0) throw rt_err("empty batch");
+    if (n > max_batch_) throw rt_err("batch of " + std::to_string(n) + " tokens exceeds max batch " + std::to_string(max_batch_));
+    if (pos + n > n_ctx_) throw rt_err("context window full (" + std::to_string(n_ctx_) + " tokens)");
+    for (size_t t = 0; t < n; t++)
+        if (tokens[t] >= m_.token_embd.rows) throw rt_err("token id " + std::to_string(tokens[t]) + " out of range");
+    const size_t m = all_logits ? n : 1;
+    if (logits_len < m * c.n_vocab) throw rt_err("logits buffer too small");
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    RIE_HIP_CHECK(hipMemcpyAsync(d_tokens_, tokens, n * 4, hipMemcpyHostToDevice, st_));
+    if (n == 1 && use_graph_ && !capture_) {
+        decode_step_graph(pos);
+    } else {
+        run_layers((int)n, pos, nullptr, all_logits, decode_split());
+    }
+    RIE_HIP_CHECK(hipMemcpyAsync(logits, d_logits_, m * c.n_vocab * 4, hipMemcpyDeviceToHost, st_));
+    RIE_HIP_CHECK(hipStreamSynchronize(st_));
+    hidden_rows_ = m;
+}
+
+// The decode step as a graph: kernels read pos from d_pos_ and the token from
+// d_tokens_[0]; the host only writes {pos} into pinned memory before a replay.
+void HipBackend::decode_step_graph(size_t pos) {
+    // the position travels as a kernel argument (copied at launch), so queued
+    // steps never share a host-side slot
+    launch_set_int(d_pos_, (int)pos, st_);
+    check_launch("set pos");
+    if (!graph_exec_) {
+        in_capture_ = true;
+        RIE_HIP_CHECK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+        try {
+            run_layers(1, 0, d_pos_, false, decode_split());
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(st_, &g);
+            if (g) (void)hipGraphDestroy(g);
+            in_capture_ = false;
+            throw;
+        }
+        RIE_HIP_CHECK(hipStreamEndCapture(st_, &graph_));
+        in_capture_ = false;
+        RIE_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+    }
+    RIE_HIP_CHECK(hipGraphLaunch(graph_exec_, st_));
+}
+
+const float *HipBackend::hidden(size_t *rows) {
+    *rows = hidden_rows_;
+    if (!hidden_rows_) return nullptr;
+    hidden_host_.resize(hidden_rows_ * m_.cfg.n_embd);
+    RIE_HIP_CHECK(hipMemcpyAsync(hidden_host_.data(), d_xn_, hidden_host_.size() * 4, hipMemcpyDeviceToHost, st_));
+    RIE_HIP_CHECK(hipStreamSynchronize(st_));
+    return hidden_host_.data();
+}
+
+uint32_t HipBackend::forward_argmax(const uint32_t *tokens, size_t n, size_t pos) {
+    const ModelConfig &c = m_.cfg;
+    hidden_rows_ = 0;
+    if (n == 0) throw rt_err("empty batch");
+    if (n > max_batch_) throw rt_err("batch of " + std::to_string(n) + " tokens exceeds max batch " + std::to_string(max_batch_));
+    if (pos + n > n_ctx_) throw rt_err("context window full (" + std::to_string(n_ctx_) + " tokens)");
+    for (size_t t = 0; t < n; t++)
+        if (tokens[t] >= m_.token_embd.rows) throw rt_err("token id " + std::to_string(tokens[t]) + " out of range");
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    RIE_HIP_CHECK(hipMemcpyAsync(d_tokens_, tokens, n * 4, hipMemcpyHostToDevice, st_));
+    if (n == 1 && use_graph_ && !capture_) {
+        decode_step_graph(pos);
+    } else {
+        run_layers((int)n, pos, nullptr, false, decode_split());
+    }
+    launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
+    check_launch("argmax");
+    uint32_t tok = 0;
+    RIE_HIP_CHECK(hipMemcpyAsync(&tok, d_tokens_, 4, hipMemcpyDeviceToHost, st_));
+    RIE_HIP_CHECK(hipStreamSynchronize(st_));
+    hidden_rows_ = 1;
+    return tok;
+}
+
+// greedy steps without host round trips: each step's argmax is written to
+// d_tokens_[0] (the next step's input) and appended to d_gen_.
+void HipBackend::generate_greedy(size_t pos, size_t n_gen, uint32_t *out) {
+    if (pos + n_gen > n_ctx_) throw rt_err("context window full (" + std::to_string(n_ctx_) + " tokens)");
+    if (n_gen == 0) return;
+    const ModelConfig &c = m_.cfg;
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    for (size_t i = 0; i < n_gen; i++) {
+        RIE_HIP_CHECK(hipMemcpyAsync(d_gen_ + i, d_tokens_, 4, hipMemcpyDeviceToDevice, st_));
+        if (use_graph_ && !capture_) {
+            decode_step_graph(pos + i);
+        } else {
+            run_layers(1, pos + i, nullptr, false, decode_split());
+        }
+        launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
+        check_launch("argmax");
+    }
+    RIE_HIP_CHECK(hipMemcpyAsync(out, d_gen_, n_gen * 4, hipMemcpyDeviceToHost, st_));
+    RIE_HIP_CHECK(hipStreamSynchronize(st_));
+    hidden_rows_ = 1;
+}
+
+void HipBackend::synchronize() { RIE_HIP_CHECK(hipStreamSynchronize(st_)); }
+
+void HipBackend::set_capture(bool on) {
+    capture_ = on;
+    for (auto &v : cap_) v.clear();
+}
+
+bool HipBackend::capture(size_t layer, int what, float *out, size_t len) {
+    if (what < 0 || what >= (int)cap_.size() || layer >= cap_[what].size()) return false;
+    const auto &v = cap_[what][layer];
+    if (v.empty() || len < v.size()) return false;
+    std::memcpy(out, v.data(), v.size() * 4);
+    return true;
+}
+
+void HipBackend::kv_layer(size_t layer, int which, uint8_t *out, size_t len, uint8_t *scales_out, size_t scales_len) {
+    if (layer >= layers_.size()) throw rt_err("layer out of range");
+    const DevLayer &D = layers_[layer];
+    const size_t bytes = m_.cfg.n_head_kv * D.slots * kv_row_bytes();
+    if (len < bytes) throw rt_err("buffer too small");
+    RIE_HIP_CHECK(hipStreamSynchronize(st_));
+    RIE_HIP_CHECK(hipMemcpy(out, which ? D.v_cache : D.k_cache, bytes, hipMemcpyDeviceToHost));
+    if (kv_type_ == 2 && scales_out) {
+        const size_t sb = m_.cfg.n_head_kv * D.slots * 2 * turbo_blocks();
+        if (scales_len < sb) throw rt_err("buffer too small");
+        RIE_HIP_CHECK(hipMemcpy(scales_out, which ? D.v_scale : D.k_scale, sb, hipMemcpyDeviceToHost));
+    }
+}
+
+void HipBackend::mark(const char *name) {
+    if (!profiling_) return;
+    hipEvent_t e;
+    RIE_HIP_CHECK(hipEventCreate(&e));
+    RIE_HIP_CHECK(hipEventRecord(e, st_));
+    marks_.emplace_back(name, e);
+}
+
+// One eager decode step per repetition at position pos, with an event after
+// every launch on the backend's stream; returns per-kernel-family totals.
+std::vector<HipBackend::KernelTime> HipBackend::profile_decode(size_t pos, int reps) {
+    if (pos + 1 > n_ctx_) throw rt_err("context window full");
+    std::vector<KernelTime> out;
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    for (int r = 0; r < reps; r++) {
+        profiling_ = true;
+        marks_.clear();
+        RIE_HIP_CHECK(hipEventCreate(&mark0_));
+        RIE_HIP_CHECK(hipEventRecord(mark0_, st_));
+        try {
+            run_layers(1, pos, nullptr, false, decode_split());
+        } catch (...) {
+            profiling_ = false;
+            throw;
+        }
+        profiling_ = false;
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        hipEvent_t prev = mark0_;
+        for (auto &m : marks_) {
+            float ms = 0;
+            RIE_HIP_CHECK(hipEventElapsedTime(&ms, prev, m.second));
+            auto it = std::find_if(out.begin(), out.end(), [&](const KernelTime &k) { return k.name == m.first; });
+            if (it == out.end()) {
+                out.push_back(KernelTime{m.first, 0, 0});
+                it = out.end() - 1;
+            }
+            it->ms += ms;
+            it->launches += 1;
+            prev = m.second;
+        }
+        (void)hipEventDestroy(mark0_);
+        for (auto &m : marks_) (void)hipEventDestroy(m.second);
+        marks_.clear();
+    }
+    return out;
+}
+
+}  // namespace rie

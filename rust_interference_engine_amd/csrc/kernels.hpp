@@ -1,0 +1,85 @@
+// kernels.hpp — host-side launchers of the gfx950 kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace rie {
+
+// ---- quant.hip ----
+void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
+                          hipStream_t st);
+void launch_rmsnorm(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *out, int ldo, int inplace_assoc,
+                    hipStream_t st);
+void launch_embed(const uint32_t *tokens, int n, const DevWeight &table, float scale, float *x, hipStream_t st);
+
+// ---- gemv.hip ----
+// Output epilogues of one GEMV segment.
+enum Epi : int { EPI_STORE = 0, EPI_ADD = 1 };
+struct GemvSeg {
+    DevWeight w;
+    float *out;   // out[t*ld + r]
+    int ld;
+    int epi;
+};
+// y_seg = W_seg · act for up to 3 segments sharing one activation batch (n_tok rows).
+// Returns false when a weight type/shape has no kernel.
+bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st);
+// h = act(gate·x) ⊙ (up·x) for gated feed-forward blocks (gelu selects GELU-tanh).
+bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
+                     hipStream_t st);
+bool gemv_supported(int ty, size_t K);
+
+// ---- attention.hip ----
+struct HeadPrepArgs {
+    float *q;            // [n][qd] in/out (rotated, scaled)
+    const float *k;      // [n][kvd]
+    const float *v;      // [n][kvd]
+    const float *bq, *bk, *bv;        // optional biases
+    const float *q_norm, *k_norm;     // optional per-head RMSNorm weights [hd]
+    const float *cos_t, *sin_t;       // rope tables [n_ctx][rope_dim/2]
+    int n_tok, pos0, n_head, n_kv, hd, rope_dim, neox;
+    float eps, attn_scale;
+    int kv_type;                      // 0 f16, 1 q8_0, 2 turbo4
+    uint8_t *k_cache, *v_cache;       // layer base: [n_kv][slots][row]
+    uint16_t *k_scale, *v_scale;      // turbo4 only: [n_kv][slots] f16 scales
+    int slots;
+    const int *d_pos0;                // optional device-resident pos0 (graph replay)
+    const float *turbo_signs;         // [hd]
+    float *k_out;                     // optional: K after norm/RoPE, [n][kvd] (parity hooks)
+};
+void launch_head_prep(const HeadPrepArgs &a, hipStream_t st);
+
+struct AttnArgs {
+    const float *q;              // [n][qd]
+    const uint8_t *k_cache, *v_cache;
+    const uint16_t *k_scale, *v_scale;
+    int n_tok, pos0, n_head, n_kv, hd, slots, window, kv_type;
+    float softcap;               // 0 = none
+    float *part;                 // [n][n_head][n_split][hd + 2]
+    int n_split;
+    float *att;                  // [n][qd] f32 output
+    ActQ8 att_q;                 // optional Q8_0 quantization of att (qs/d/s/isum) when att_fmt == ACT_Q8_0
+    int att_fmt;
+    const int *d_pos0;
+    const float *turbo_signs;
+};
+void launch_attention(const AttnArgs &a, hipStream_t st);
+
+// ---- misc.hip ----
+void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st);
+void launch_add_inplace(float *x, const float *y, size_t n, float scale, hipStream_t st);
+void launch_scale(float *x, size_t n, float div, hipStream_t st);
+void launch_set_int(int *p, int v, hipStream_t st);
+void launch_softcap(float *x, size_t n, float cap, hipStream_t st);
+void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, const ActQ8 &act, hipStream_t st);
+// MoE routing: softmax over n_exp logits per token, top-k with index tie-break, renorm.
+void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
+                      hipStream_t st);
+
+// ---- gemm.hip (prefill, int8 MFMA) ----
+bool gemm_supported(int ty, size_t K);
+bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st);
+bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
+                     float *scratch, hipStream_t st);
+
+}  // namespace rie

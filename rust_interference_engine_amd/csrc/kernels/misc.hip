@@ -1,0 +1,148 @@
+// misc.hip — greedy argmax, elementwise epilogues and MoE routing for gfx950.
+#include "../common.hpp"
+#include "../device.hpp"
+#include "../kernels.hpp"
+
+namespace rie {
+
+// sampler.rs:199-209: the first index holding the strict maximum.  NaN never wins.
+__device__ __forceinline__ void amax_merge(float &v, int &i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_stage1(const float *__restrict__ x, int n, int *pidx, float *pval) {
+    const int tid = threadIdx.x;
+    const int per = (n + gridDim.x - 1) / gridDim.x;
+    const int a = blockIdx.x * per, b = min(n, a + per);
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = a + tid; i < b; i += 256) {
+        const float xv = x[i];
+        if (xv > v) {  // first hit within this lane's strided scan is the smallest index
+            v = xv;
+            idx = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = v;
+        si[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; w++) amax_merge(v, idx, sv[w], si[w]);
+        pval[blockIdx.x] = v;
+        pidx[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float *pval, int n_part, uint32_t *out) {
+    const int tid = threadIdx.x;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = tid; i < n_part; i += 64) amax_merge(v, idx, pval[i], pidx[i]);
+    for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if (tid == 0) *out = idx == 0x7fffffff ? 0u : (uint32_t)idx;
+}
+
+void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
+    hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx);
+}
+
+__global__ void add_kernel(float *x, const float *y, size_t n, float scale) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = scale == 1.0f ? x[i] + y[i] : x[i] + y[i] * scale;
+}
+
+void launch_add_inplace(float *x, const float *y, size_t n, float scale, hipStream_t st) {
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, n, scale);
+}
+
+__global__ void div_kernel(float *x, size_t n, float div) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] /= div;
+}
+
+void launch_scale(float *x, size_t n, float div, hipStream_t st) {
+    hipLaunchKernelGGL(div_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, div);
+}
+
+__global__ void set_int_kernel(int *p, int v) { *p = v; }
+
+void launch_set_int(int *p, int v, hipStream_t st) { hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, p, v); }
+
+__global__ void softcap_kernel(float *x, size_t n, float cap) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = cap * tanhf(x[i] / cap);
+}
+
+void launch_softcap(float *x, size_t n, float cap, hipStream_t st) {
+    hipLaunchKernelGGL(softcap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, cap);
+}
+
+void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, const ActQ8 &act, hipStream_t st) {
+    launch_rmsnorm_quant(x, ldx, nullptr, 0.0f, n_rows, K, nullptr, fmt, act, st);
+}
+
+// MoE routing (model/cpu.rs:487-501): softmax over the router logits, sort by
+// probability descending with the lower expert index first on ties, keep the
+// top k, optionally renormalize by their sum taken in sorted order.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_exp, int k, int norm_topk, int unit_weights, int *sel,
+                                                       float *wgt) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    __shared__ float pr[512];
+    const float *l = logits + (size_t)t * n_exp;
+    float mx = -INFINITY;
+    for (int i = lane; i < n_exp; i += 64) mx = fmaxf(mx, l[i]);
+    mx = wave_max(mx, 64);
+    for (int i = lane; i < n_exp; i += 64) pr[i] = expf(l[i] - mx);
+    __syncthreads();
+    if (lane == 0) {  // sequential sum and scaling, ops.rs:38-49
+        float sum = 0.0f;
+        for (int i = 0; i < n_exp; i++) sum += pr[i];
+        const float inv = 1.0f / sum;
+        for (int i = 0; i < n_exp; i++) pr[i] *= inv;
+    }
+    __syncthreads();
+    __shared__ int chosen[64];
+    __shared__ float cval[64];
+    for (int j = 0; j < k; j++) {
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        for (int i = lane; i < n_exp; i += 64) {
+            bool taken = false;
+            for (int q = 0; q < j; q++) taken |= chosen[q] == i;
+            if (!taken) amax_merge(v, idx, pr[i], i);
+        }
+        for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+        if (lane == 0) {
+            chosen[j] = idx;
+            cval[j] = v;
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        float norm = 1.0f;
+        if (norm_topk) {
+            norm = 0.0f;
+            for (int j = 0; j < k; j++) norm += cval[j];
+        }
+        for (int j = 0; j < k; j++) {
+            sel[(size_t)t * k + j] = chosen[j];
+            wgt[(size_t)t * k + j] = unit_weights ? 1.0f : cval[j] / norm;
+        }
+    }
+}
+
+void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
+                      hipStream_t st) {
+    hipLaunchKernelGGL(moe_route_kernel, dim3(n_tok), dim3(64), 0, st, logits, n_exp, k, norm_topk, unit_weights, sel, wgt);
+}
+
+}  // namespace rie

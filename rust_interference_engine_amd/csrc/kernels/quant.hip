@@ -1,0 +1,220 @@
+// quant.hip — RMSNorm + on-the-fly int8 activation quantization, and token
+// embedding dequantization, for gfx950.
+//
+// Q8_0 (32-value blocks) follows RIE's x86 quantizer (kernels/avx2.rs:153-184):
+//   amax = max|x|, d = amax/127, id = d != 0 ? 1/d : 0, q = RNE(x·id) clamped to
+//   ±127, s = d·Σ(unclamped q).  Half a wavefront (32 lanes) owns one block.
+// Q8_K (256-value blocks) follows quant/mod.rs:191-218: the first element with
+//   the strictly largest |x| sets max, iscale = -127/max, q = round-half-away,
+//   bsums over 16, d = 1/iscale.  One wavefront owns one block.
+// Division and sqrt are the correctly rounded IEEE operations (no fast-math), so
+// identical f32 inputs give bit-identical codes and scales.
+#include "../common.hpp"
+#include "../device.hpp"
+#include "../kernels.hpp"
+
+namespace rie {
+
+template <int FMT>
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w,
+                                                            float eps, int E, float *__restrict__ xn, ActQ8 act) {
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *xr = x + (size_t)row * ldx;
+    __shared__ float red[4];
+    __shared__ float s_scale;
+    float scale = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int i = tid; i < E; i += 256) ss = fmaf(xr[i], xr[i], ss);
+        ss = wave_sum(ss, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) {
+            float t = (red[0] + red[1]) + (red[2] + red[3]);
+            s_scale = 1.0f / sqrtf(t / (float)E + eps);
+        }
+        __syncthreads();
+        scale = s_scale;
+    }
+    if (FMT == ACT_Q8_0) {
+        const int hw = tid >> 5, j = tid & 31;
+        const int nb = E >> 5;
+        for (int b = hw; b < nb; b += 8) {
+            const int i = (b << 5) + j;
+            float y = w ? xr[i] * scale * w[i] : xr[i];
+            if (xn) xn[(size_t)row * E + i] = y;
+            float amax = fabsf(y);
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int q = (int)rintf(y * id);
+            const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
+            int su = q, sc = qc;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {
+                su += __shfl_xor(su, o, 64);
+                sc += __shfl_xor(sc, o, 64);
+            }
+            act.qs[(size_t)row * E + i] = (int8_t)qc;
+            if (j == 0) {
+                const size_t bi = (size_t)row * nb + b;
+                act.d[bi] = d;
+                if (act.s) act.s[bi] = d * (float)su;
+                if (act.isum) act.isum[bi] = sc;
+            }
+        }
+    } else {
+        const int wv = tid >> 6, l = tid & 63;
+        const int nb = E >> 8;
+        for (int b = wv; b < nb; b += 4) {
+            const int i0 = (b << 8) + (l << 2);
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                y[e] = w ? xr[i0 + e] * scale * w[i0 + e] : xr[i0 + e];
+                if (xn) xn[(size_t)row * E + i0 + e] = y[e];
+            }
+            float amax = 0.0f, mx = 0.0f;
+            int idx = 0x7fffffff;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (fabsf(y[e]) > amax) {
+                    amax = fabsf(y[e]);
+                    mx = y[e];
+                    idx = (l << 2) + e;
+                }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                float oa = __shfl_xor(amax, o, 64), om = __shfl_xor(mx, o, 64);
+                int oi = __shfl_xor(idx, o, 64);
+                if (oa > amax || (oa == amax && oi < idx)) {
+                    amax = oa;
+                    mx = om;
+                    idx = oi;
+                }
+            }
+            int8_t *qo = act.qs + (size_t)row * E + i0;
+            const size_t bi = (size_t)row * nb + b;
+            if (amax == 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) qo[e] = 0;
+                if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = 0;
+                if (l == 0) act.d[bi] = 0.0f;
+                continue;
+            }
+            const float iscale = -127.0f / mx;
+            int s4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int q = (int)roundf(iscale * y[e]);
+                q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                qo[e] = (int8_t)q;
+                s4 += q;
+            }
+            s4 += __shfl_xor(s4, 1, 64);
+            s4 += __shfl_xor(s4, 2, 64);
+            if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = (int16_t)s4;
+            if (l == 0) act.d[bi] = 1.0f / iscale;
+        }
+    }
+}
+
+void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
+                          hipStream_t st) {
+    if (fmt == ACT_Q8_0)
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+    else
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8K>, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+}
+
+// RMSNorm without quantization (f32 out), one row per workgroup: ops.rs:7-14
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w, float eps,
+                                                      int E, float *__restrict__ out, int ldo, int inplace_assoc) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (size_t)row * ldx;
+    __shared__ float red[4];
+    __shared__ float s_scale;
+    float ss = 0.0f;
+    for (int i = tid; i < E; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = wave_sum(ss, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    if (tid == 0) s_scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)E + eps);
+    __syncthreads();
+    const float scale = s_scale;
+    float *o = out + (size_t)row * ldo;
+    for (int i = tid; i < E; i += 256) o[i] = inplace_assoc ? xr[i] * (scale * w[i]) : xr[i] * scale * w[i];
+}
+
+void launch_rmsnorm(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *out, int ldo, int inplace_assoc,
+                    hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, out, ldo, inplace_assoc);
+}
+
+// ---- token embedding: dequantize_row (quant/reference.rs:53-215) ---------------
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t *__restrict__ tokens, const uint8_t *__restrict__ table, int ty,
+                                                    int E, size_t rb, float scale, float *__restrict__ x) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= E) return;
+    const uint8_t *row = table + (size_t)tokens[t] * rb;
+    float y = 0.0f;
+    switch (ty) {
+    case T_F32: y = ((const float *)row)[i]; break;
+    case T_F16: y = h2f(((const uint16_t *)row)[i]); break;
+    case T_Q4_0: {
+        const uint8_t *b = row + (i >> 5) * 18;
+        const int j = i & 31;
+        const float d = h2f(b[0] | (b[1] << 8));
+        const int q = j < 16 ? (b[2 + j] & 15) : (b[2 + j - 16] >> 4);
+        y = (float)(q - 8) * d;
+        break;
+    }
+    case T_Q8_0: {
+        const uint8_t *b = row + (i >> 5) * 34;
+        y = (float)(int8_t)b[2 + (i & 31)] * h2f(b[0] | (b[1] << 8));
+        break;
+    }
+    case T_Q4_K: {
+        const uint8_t *b = row + (i >> 8) * 144;
+        const int r = i & 255, j = r >> 6, l = r & 63;
+        const float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        const uint8_t *q = b + 4;
+        const int sj = 2 * j + (l >= 32);
+        uint8_t sc, mn;
+        if (sj < 4) {
+            sc = q[sj] & 63;
+            mn = q[sj + 4] & 63;
+        } else {
+            sc = (q[sj + 4] & 0xF) | ((q[sj - 4] >> 6) << 4);
+            mn = (q[sj + 4] >> 4) | ((q[sj] >> 6) << 4);
+        }
+        const uint8_t qb = b[16 + 32 * j + (l & 31)];
+        const int v = l < 32 ? (qb & 15) : (qb >> 4);
+        y = d * (float)sc * (float)v - dmin * (float)mn;
+        break;
+    }
+    case T_Q6_K: {
+        const uint8_t *b = row + (i >> 8) * 210;
+        const int r = i & 255, n = r >> 7, k = (r & 127) >> 5, l = r & 31;
+        const uint8_t qlb = b[64 * n + l + 32 * (k & 1)];
+        const uint8_t qhb = b[128 + 32 * n + l];
+        const int q = (((k >= 2) ? (qlb >> 4) : (qlb & 15)) | (((qhb >> (2 * k)) & 3) << 4)) - 32;
+        const float d = h2f(b[208] | (b[209] << 8));
+        y = d * (float)(int8_t)b[192 + 8 * n + 2 * k + (l >> 4)] * (float)q;
+        break;
+    }
+    default: break;
+    }
+    if (scale != 1.0f) y *= scale;
+    x[(size_t)t * E + i] = y;
+}
+
+void launch_embed(const uint32_t *tokens, int n, const DevWeight &table, float scale, float *x, hipStream_t st) {
+    const int E = (int)table.cols;
+    hipLaunchKernelGGL(embed_kernel, dim3((E + 255) / 256, n), dim3(256), 0, st, tokens, table.data, table.ty, E, table.rb(), scale, x);
+}
+
+}  // namespace rie

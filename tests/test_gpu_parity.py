@@ -1,0 +1,297 @@
+"""Parity of the HIP path (through the C ABI) with the oracle on MI355X.
+
+Bit-exact on identical inputs: Q8_0 / Q8_K activation codes and scales, the
+per-block integer dot products, f16 / Q8_0 / Turbo4 KV codes, argmax.
+Float results: GEMV rows within the reference's kernel tolerance
+(tests/kernels.rs:60: 1e-4·Σ|w·x| + 1e-5), whole-model logits within the
+reference's whole-model tolerances (tests/model.rs:340-375: 3e-3 f16, 0.03
+quantized; 0.05 Q8_0 KV), greedy sequences identical.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+import rust_interference_engine_amd as R  # noqa: E402
+from rust_interference_engine_amd import synth  # noqa: E402
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    assert torch.cuda.is_available(), "these tests need the MI355X"
+    return torch.device("cuda:0")
+
+
+def dev(a: np.ndarray, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def _quant_on_gpu(x, fmt, cuda, w=None, eps=1e-6):
+    n, k = x.shape
+    L = R.lib()
+    xd = dev(x.astype(np.float32), cuda)
+    wd = dev(w.astype(np.float32), cuda) if w is not None else None
+    qs = torch.zeros(n * k, dtype=torch.int8, device=cuda)
+    xn = torch.zeros(n * k, dtype=torch.float32, device=cuda)
+    if fmt == 1:
+        d = torch.zeros(n * k // 32, dtype=torch.float32, device=cuda)
+        s = torch.zeros_like(d)
+        isum = torch.zeros(n * k // 32, dtype=torch.int32, device=cuda)
+        rc = L.rie_hip_k_rmsnorm_quant(xd.data_ptr(), wd.data_ptr() if wd is not None else None, eps, n, k, 1, xn.data_ptr(),
+                                       qs.data_ptr(), d.data_ptr(), s.data_ptr(), isum.data_ptr(), None)
+        assert rc == 0
+        return dict(qs=host(qs).reshape(n, k), d=host(d), s=host(s), isum=host(isum), xn=host(xn).reshape(n, k),
+                    dev=(qs, d, s, isum, None))
+    d = torch.zeros(n * k // 256, dtype=torch.float32, device=cuda)
+    bs = torch.zeros(n * k // 16, dtype=torch.int16, device=cuda)
+    rc = L.rie_hip_k_rmsnorm_quant(xd.data_ptr(), wd.data_ptr() if wd is not None else None, eps, n, k, 2, xn.data_ptr(),
+                                   qs.data_ptr(), d.data_ptr(), None, None, bs.data_ptr())
+    assert rc == 0
+    return dict(qs=host(qs).reshape(n, k), d=host(d), bsums=host(bs), xn=host(xn).reshape(n, k), dev=(qs, d, None, None, bs))
+
+
+def _act_inputs(rng, n, k):
+    x = (rng.standard_normal((n, k)) * rng.uniform(0.01, 20, (n, 1))).astype(np.float32)
+    x[0, :32] = 0.0                                   # zero block
+    x[0, 32:64] = np.arange(32, dtype=np.float32) - 15.5
+    x[0, 64] = 127.0                                  # exact ties at id = 1
+    x[0, 65:72] = [2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -126.5]
+    return x
+
+
+def test_q8_0_activation_codes_bit_exact(oracle, cuda):
+    rng = np.random.default_rng(0)
+    for n, k in ((1, 256), (3, 4096), (5, 14336)):
+        x = _act_inputs(rng, n, k)
+        g = _quant_on_gpu(x, 1, cuda)
+        for t in range(n):
+            ref = oracle.quantize_q8_0(x[t])
+            assert np.array_equal(g["qs"][t], ref["qs"].reshape(-1))
+            nb = k // 32
+            assert np.array_equal(g["d"][t * nb:(t + 1) * nb].view(np.uint32), ref["d"].view(np.uint32))
+            assert np.array_equal(g["s"][t * nb:(t + 1) * nb].view(np.uint32), ref["s"].view(np.uint32))
+            assert np.array_equal(g["isum"][t * nb:(t + 1) * nb], ref["qs"].astype(np.int32).sum(axis=1))
+
+
+def test_q8_k_activation_codes_bit_exact(oracle, cuda):
+    rng = np.random.default_rng(1)
+    for n, k in ((1, 256), (4, 4096)):
+        x = _act_inputs(rng, n, k)
+        x[n - 1, 256:512] = 0.0
+        x[n - 1, 512 + 3], x[n - 1, 512 + 10] = -7.0, 7.0  # first-max tie
+        g = _quant_on_gpu(x, 2, cuda)
+        for t in range(n):
+            ref = oracle.quantize_q8_k(x[t])
+            nb = k // 256
+            assert np.array_equal(g["qs"][t], ref["qs"].reshape(-1))
+            assert np.array_equal(g["d"][t * nb:(t + 1) * nb].view(np.uint32), ref["d"].view(np.uint32))
+            assert np.array_equal(g["bsums"][t * k // 16:(t + 1) * k // 16], ref["bsums"].reshape(-1))
+
+
+def test_rmsnorm_then_quant(oracle, cuda):
+    """normalized rows within f32 rounding of ops.rs:7-14; codes bit-exact on the GPU's own rows"""
+    rng = np.random.default_rng(2)
+    n, k = 4, 4096
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    w = (1 + 0.1 * rng.uniform(-1, 1, k)).astype(np.float32)
+    g = _quant_on_gpu(x, 1, cuda, w=w)
+    L = oracle.lib()
+    for t in range(n):
+        ref = np.zeros(k, np.float32)
+        L.or_rmsnorm(oracle.ptr(ref), oracle.ptr(np.ascontiguousarray(x[t])), oracle.ptr(w), k, 1e-6)
+        assert np.abs(g["xn"][t] - ref).max() <= 4e-7 * np.abs(ref).max()
+        assert np.array_equal(g["qs"][t], oracle.quantize_q8_0(g["xn"][t])["qs"].reshape(-1))
+
+
+def _gemv(ty, w, rows, k, act, act_f32, n_tok, cuda, gemm=False):
+    L = R.lib()
+    wd = dev(w, cuda)
+    out = torch.zeros(n_tok * rows, dtype=torch.float32, device=cuda)
+    qs, d, s, isum, bs = act if act is not None else (None,) * 5
+    p = lambda t: t.data_ptr() if t is not None else None
+    fd = dev(act_f32, cuda) if act_f32 is not None else None
+    if gemm:
+        rc = L.rie_hip_k_gemm(ty, wd.data_ptr(), rows, k, p(qs), p(d), p(s), p(isum), p(bs), n_tok, out.data_ptr())
+    else:
+        rc = L.rie_hip_k_gemv(ty, wd.data_ptr(), rows, k, p(qs), p(d), p(s), p(isum), p(bs), p(fd), n_tok, out.data_ptr())
+    assert rc == 0
+    return host(out).reshape(n_tok, rows)
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0, Q4_K, Q6_K, F32, F16])
+def test_gemv_matches_oracle_rows(oracle, cuda, ty):
+    import ggml_np as G
+    r = oracle.Rng(21 + ty)
+    for k in (256, 2048, 4096):
+        rows = 96
+        w = r.random_weight(ty, rows, k)
+        for n_tok in (1, 3, 6):
+            x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
+            fmt = 0 if ty in (F32, F16) else (2 if ty in (Q4_K, Q6_K) else 1)
+            act = _quant_on_gpu(x, fmt, cuda)["dev"] if fmt else None
+            got = _gemv(ty, w, rows, k, act, x if fmt == 0 else None, n_tok, cuda)
+            wf = G.dequantize(ty, w, rows * k).reshape(rows, k).astype(np.float64)
+            for t in range(n_tok):
+                a = oracle.quantize_act(ty, x[t])
+                rb = G.row_bytes(ty, k)
+                want = np.array([oracle.vec_dot(ty, w[i * rb:(i + 1) * rb], a, k) for i in range(rows)])
+                mag = np.abs(wf * x[t].astype(np.float64)).sum(axis=1)
+                assert np.all(np.abs(got[t] - want) <= 1e-5 * mag + 1e-6), (ty, k, n_tok)
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
+def test_gemv_per_block_integer_dots_exact(oracle, cuda, ty):
+    """With one non-zero activation block the row result is one rounding of
+    (d_w·d_a)·idot, so it pins every per-block int32 dot exactly."""
+    r = oracle.Rng(5)
+    k, rows = 2048, 64
+    w = r.random_weight(ty, rows, k)
+    rng = np.random.default_rng(7)
+    for b in (0, 1, 17, k // 32 - 1):
+        x = np.zeros((1, k), np.float32)
+        x[0, b * 32:(b + 1) * 32] = rng.standard_normal(32) * 3
+        act = _quant_on_gpu(x, 1, cuda)
+        got = _gemv(ty, w, rows, k, act["dev"], None, 1, cuda)[0]
+        a = oracle.quantize_q8_0(x[0])
+        rb = (18 if ty == Q4_0 else 34) * k // 32
+        for i in range(rows):
+            idots = oracle.block_idots(ty, w[i * rb:(i + 1) * rb], a, k)
+            blk = w[i * rb + b * (rb * 32 // k): i * rb + b * (rb * 32 // k) + 2]
+            dw = np.frombuffer(blk.tobytes(), np.float16)[0].astype(np.float32)
+            want = np.float32(np.float32(dw * a["d"][b]) * np.float32(idots[b]))
+            assert got[i] == want, (b, i)
+
+
+def test_argmax_first_index(oracle, cuda):
+    L = R.lib()
+    rng = np.random.default_rng(3)
+    for n in (10, 128256, 151936):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[n // 3] = x[2 * n // 3] = x.max() + 1  # tie: the first wins
+        xd = dev(x, cuda)
+        out = torch.zeros(1, dtype=torch.int32, device=cuda)
+        assert L.rie_hip_k_argmax(xd.data_ptr(), n, out.data_ptr()) == 0
+        assert int(host(out)[0]) == oracle.argmax(x) == n // 3
+
+
+# ---- whole model ------------------------------------------------------------------------------
+CASES = [
+    ("llama", Q4_0, 0, 0.03), ("llama", Q8_0, 0, 0.03), ("llama", Q4_K, 0, 0.03), ("llama", Q6_K, 0, 0.03),
+    ("llama", F16, 0, 3e-3), ("llama", F32, 0, 3e-3), ("qwen3", Q4_0, 0, 0.03), ("qwen2", Q4_0, 0, 0.03),
+    ("gemma3", Q4_0, 0, 0.03), ("granite", F16, 0, 3e-3), ("phi3", Q4_0, 0, 0.03), ("gemma2", F16, 0, 3e-3),
+    ("llama", Q4_0, 1, 0.05), ("llama", Q4_0, 2, 0.05), ("qwen3", Q4_K, 2, 0.05),
+]
+
+
+def _pair(oracle, arch, ty, kv, n_ctx=64, max_batch=4, mutate=None):
+    spec = synth.tiny(arch, ty)
+    if mutate:
+        mutate(spec)
+    gguf = synth.build(spec)
+    g = R.HipBackend(gguf, n_ctx=n_ctx, max_batch=max_batch, kv_type=kv)
+    o = oracle.Backend(oracle.Model(gguf), n_ctx, max_batch, kv, n_threads=4)
+    return spec, g, o
+
+
+@pytest.mark.parametrize("arch,ty,kv,tol", CASES)
+def test_model_logits_match_oracle(oracle, cuda, arch, ty, kv, tol):
+    from naive_model import max_rel_err
+    mut = (lambda s: setattr(s, "rope_dim", 32)) if arch == "phi3" else None
+    spec, g, o = _pair(oracle, arch, ty, kv, mutate=mut)
+    nv = spec.n_vocab
+    toks = [(i * 37 + 5) % nv for i in range(13)]
+    pos = 0
+    while pos < len(toks):  # batched prefill, all logits (tests/model.rs:314-329)
+        end = min(pos + 4, len(toks))
+        lg = g.forward(toks[pos:end], pos, True)
+        lo = o.forward(toks[pos:end], pos, True)
+        for t in range(end - pos):
+            err = max_rel_err(lg[t * nv:(t + 1) * nv], lo[t * nv:(t + 1) * nv])
+            assert err < tol, f"{arch} {ty} kv{kv}: batched token {pos + t}: {err}"
+        pos = end
+    spec, g, o = _pair(oracle, arch, ty, kv, max_batch=1, mutate=mut)
+    for t, tok in enumerate(toks):  # token-by-token decode (graph replay)
+        err = max_rel_err(g.forward([tok], t), o.forward([tok], t))
+        assert err < tol, f"{arch} {ty} kv{kv}: decode token {t}: {err}"
+
+
+@pytest.mark.parametrize("kv", [0, 1, 2])
+def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
+    """The cache rows the GPU writes equal the reference encoders applied to the
+    GPU's own post-RoPE K and V (f16 RNE; store_q8_0 cpu.rs:637-647; quantize_4
+    turbo.rs:166-171)."""
+    spec, g, _ = _pair(oracle, "qwen3", Q4_0, kv, n_ctx=32, max_batch=4)
+    g.set_capture(True)
+    toks = [3, 77, 150, 9]
+    g.forward(toks, 0)
+    hd, nkv = spec.head_dim, spec.n_head_kv
+    for layer in range(spec.n_layer):
+        kpost = g.capture(layer, 4, 4 * nkv * hd).reshape(4, nkv, hd)
+        vpost = g.capture(layer, 5, 4 * nkv * hd).reshape(4, nkv, hd)
+        for which, src in ((0, kpost), (1, vpost)):
+            rows, scales = g.kv_layer(layer, which, nkv, 32)
+            for t in range(4):
+                for h in range(nkv):
+                    x = src[t, h]
+                    if kv == 0:
+                        want = x.astype(np.float16).view(np.uint8)
+                        assert np.array_equal(rows[h, t], want)
+                    elif kv == 1:
+                        assert np.array_equal(rows[h, t], oracle.quantize_weights(Q8_0, x))
+                    else:
+                        ref = oracle.turbo_quantize(x)
+                        assert np.array_equal(rows[h, t], ref[2:]) and scales[h, t] == ref[:2].view(np.uint16)[0]
+
+
+def test_greedy_sequence_matches_oracle_128_steps(oracle, cuda):
+    spec, g, o = _pair(oracle, "llama", Q4_0, 0, n_ctx=256, max_batch=16)
+    prompt = [(i * 7919 + 13) % spec.n_vocab for i in range(16)]
+    want, margins, _ = o.greedy(prompt, 128)
+    got = R.Engine(g).greedy(prompt, 128)
+    if not np.array_equal(got, want):
+        i = int(np.argmax(got != want))
+        pytest.fail(f"greedy diverges at step {i}: gpu {got[i]} cpu {want[i]}, cpu top-2 margin {margins[i]:.3g}")
+
+
+def test_graph_replay_equals_eager(oracle, cuda):
+    spec = synth.tiny("qwen3", Q4_0)
+    gguf = synth.build(spec)
+    a = R.HipBackend(gguf, n_ctx=64, max_batch=4, use_graph=True)
+    b = R.HipBackend(gguf, n_ctx=64, max_batch=4, use_graph=False)
+    toks = [5, 9, 200, 7, 31, 64]
+    for i, t in enumerate(toks):
+        assert np.array_equal(a.forward([t], i), b.forward([t], i))
+
+
+def test_hidden_and_error_contract(oracle, cuda):
+    spec, g, o = _pair(oracle, "llama", Q4_0, 0, n_ctx=16, max_batch=4)
+    assert g.hidden() is None
+    g.forward([1, 2, 3], 0, True)
+    o.forward([1, 2, 3], 0, True)
+    h, ho = g.hidden(), o.hidden()
+    assert h.shape == ho.shape == (3 * spec.n_embd,)
+    assert np.abs(h - ho).max() < 1e-3 * np.abs(ho).max()
+    for toks, pos, msg in (([], 0, "empty batch"), ([1] * 5, 0, "exceeds max batch"), ([1, 2], 15, "context window full"),
+                           ([999], 0, "out of range")):
+        with pytest.raises(R.RieError, match=msg) as ei:
+            g.forward(toks, pos)
+        assert ei.value.kind == "Runtime"
+    with pytest.raises(R.RieError, match="logits buffer too small"):
+        g.forward([1, 2], 0, logits=np.zeros(10, np.float32))
+
+
+def test_engine_prefix_reuse(oracle, cuda):
+    spec = synth.tiny("llama", Q4_0)
+    e = R.Engine(R.HipBackend(synth.build(spec), n_ctx=64, max_batch=8))
+    toks = [1, 5, 9, 33, 2, 8]
+    assert e.eval_tokens(toks) == 0
+    first = e.logits().copy()
+    assert e.eval_tokens(toks) == 5  # everything but the last token is reused
+    assert np.array_equal(e.logits(), first)
