@@ -292,7 +292,7 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     const ActQ8 &a = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
     bool done = false;
     if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
-    if (!done && !launch_gemv_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, st_))
+    if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, st_))
         throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
     check_launch("ffn glu");
     mark("matmul_gate_up_glu");

@@ -25,8 +25,8 @@ struct GemvSeg {
 // Returns false when a weight type/shape has no kernel.
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st);
 // h = act(gate·x) ⊙ (up·x) for gated feed-forward blocks (gelu selects GELU-tanh).
-bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                     hipStream_t st);
+bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
+                     int ld, int gelu, hipStream_t st);
 bool gemv_supported(int ty, size_t K);
 
 // ---- attention.hip ----

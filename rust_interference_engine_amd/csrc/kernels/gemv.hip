@@ -310,7 +310,18 @@ static bool dispatch(int ty, const GemvP &p, hipStream_t st) {
     }
 }
 
+// The operands a weight type reads must exist: a missing activation array is a
+// host-side error, never a launch.
+static bool operands_ok(int ty, const ActQ8 &act, const float *act_f32) {
+    switch (act_format(ty)) {
+    case ACT_F32: return act_f32 != nullptr;
+    case ACT_Q8_0: return act.qs && act.d && (ty != T_Q4_0 || act.isum);
+    default: return act.qs && act.d && act.bsums;
+    }
+}
+
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st) {
+    if (n_tok < 1) return false;
     // segments of one launch must share a weight type; split otherwise
     int i = 0;
     while (i < nseg) {
@@ -320,7 +331,9 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
         p.nseg = j - i;
         p.total_rows = 0;
         for (int s = i; s < j; s++) {
-            if (!gemv_supported(segs[s].w.ty, K) || segs[s].w.cols != (size_t)K) return false;
+            if (!gemv_supported(segs[s].w.ty, K) || segs[s].w.cols != (size_t)K || !segs[s].w.data || !segs[s].out ||
+                !operands_ok(segs[s].w.ty, act, act_f32))
+                return false;
             p.seg[s - i] = SegP{segs[s].w.data, segs[s].w.rb(), (int)segs[s].w.rows, segs[s].out, segs[s].ld, segs[s].epi};
             p.total_rows += (int)segs[s].w.rows;
         }
@@ -335,16 +348,18 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
     return true;
 }
 
-bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                     hipStream_t st) {
-    if (gate.ty != up.ty || gate.rows != up.rows || !gemv_supported(gate.ty, K)) return false;
+bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
+                     int ld, int gelu, hipStream_t st) {
+    if (gate.ty != up.ty || gate.rows != up.rows || !gemv_supported(gate.ty, K) || gate.cols != (size_t)K || up.cols != (size_t)K ||
+        !gate.data || !up.data || !h || n_tok < 1 || !operands_ok(gate.ty, act, act_f32))
+        return false;
     GemvP p{};
     p.nseg = 2;
     p.seg[0] = SegP{gate.data, gate.rb(), (int)gate.rows, h, ld, EPI_STORE};
     p.seg[1] = SegP{up.data, up.rb(), (int)up.rows, h, ld, EPI_STORE};
     p.total_rows = (int)gate.rows;
     p.act = act;
-    p.actf = nullptr;
+    p.actf = act_f32;
     p.n_tok = n_tok;
     p.K = K;
     p.glu = gelu ? 2 : 1;
