@@ -42,6 +42,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     if (kv == 1 && c.head_dim % 32 != 0) kv = 0;
     if (kv == 2 && (c.head_dim % 32 != 0 || c.head_dim > 512)) kv = 0;
     kv_type_ = kv;
+    if (c.head_dim % 8 != 0) throw Error{E_UNSUPPORTED, "unsupported: head dim " + std::to_string(c.head_dim) + " (not a multiple of 8) on the HIP backend"};
     if (c.head_dim > 256) throw Error{E_UNSUPPORTED, "unsupported: head dim " + std::to_string(c.head_dim) + " on the HIP backend"};
     if (c.n_head / c.n_head_kv > 8) throw Error{E_UNSUPPORTED, "unsupported: more than 8 query heads per KV head"};
 
@@ -193,6 +194,12 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     act0_.d = dalloc<float>(allocs_, kq / 32);
     act0_.s = dalloc<float>(allocs_, kq / 32);
     act0_.isum = dalloc<int32_t>(allocs_, kq / 32);
+    // Q8_0 of the single-token FFN hidden, written by the gate/up kernel while
+    // it still reads act0_
+    act_h_.qs = dalloc<int8_t>(allocs_, ff_max_);
+    act_h_.d = dalloc<float>(allocs_, ff_max_ / 32 + 1);
+    act_h_.s = dalloc<float>(allocs_, ff_max_ / 32 + 1);
+    act_h_.isum = dalloc<int32_t>(allocs_, ff_max_ / 32 + 1);
     actk_.qs = dalloc<int8_t>(allocs_, kq);
     actk_.d = dalloc<float>(allocs_, kq / 256 + 1);
     actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
@@ -270,11 +277,11 @@ void HipBackend::prepare(const float *x, const float *norm, int n, int K, const 
 
 // matmul_multi (matmul.rs:136-176): decode-sized batches stream the weights
 // through the GEMV kernels; prompt batches go to the int8 MFMA GEMM.
-void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K) {
+void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0) {
     // group by activation format: each launch reads one activation batch
     for (int i = 0; i < nseg; i++) {
         const int fmt = act_format(segs[i].w.ty);
-        const ActQ8 &a = fmt == ACT_Q8K ? actk_ : act0_;
+        const ActQ8 &a = fmt == ACT_Q8K ? actk_ : (act_q8_0 ? *act_q8_0 : act0_);
         bool done = false;
         if (n > 8 && gemm_supported(segs[i].w.ty, K)) done = launch_gemm(&segs[i], 1, a, n, K, st_);
         if (!done && !launch_gemv(&segs[i], 1, a, d_xn_, n, K, st_))
@@ -292,16 +299,22 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     const ActQ8 &a = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
     bool done = false;
     if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
-    if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, st_))
+    const int fmt = act_format(L.down.ty);
+    // single-token Q8_0 down projection: the gate/up kernel quantizes h itself
+    bool h_quantized = false;
+    if (!done && n == 1 && fmt == ACT_Q8_0 && ff % 32 == 0)
+        h_quantized = done = launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, &act_h_, st_);
+    if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, nullptr, st_))
         throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
     check_launch("ffn glu");
     mark("matmul_gate_up_glu");
-    const int fmt = act_format(L.down.ty);
-    if (fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_h_, (size_t)n * ff * 4, hipMemcpyDeviceToDevice, st_));
-    else launch_quant_only(d_h_, ff, n, ff, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
-    mark("quant");
+    if (!h_quantized) {
+        if (fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_h_, (size_t)n * ff * 4, hipMemcpyDeviceToDevice, st_));
+        else launch_quant_only(d_h_, ff, n, ff, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+        mark("quant");
+    }
     GemvSeg s{L.down, out, E, epi};
-    matmul(&s, 1, n, ff);
+    matmul(&s, 1, n, ff, h_quantized ? &act_h_ : nullptr);
     mark("matmul_down");
 }
 

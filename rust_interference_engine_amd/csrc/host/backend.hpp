@@ -85,7 +85,7 @@ class HipBackend {
     const float *dev_vec(const HostWeight &w);
     void run_layers(int n, size_t pos0, const int *d_pos0, bool all_logits, int n_split);
     void prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32);
-    void matmul(const GemvSeg *segs, int nseg, int n, int K);
+    void matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0 = nullptr);
     void ffn_dense(const DevLayer &L, int n, float *out_resid, int epi);
     void ffn_moe(const DevLayer &L, int n);
     void head(int first, int m);
@@ -120,6 +120,7 @@ class HipBackend {
           *d_o_ = nullptr, *d_logits_ = nullptr, *d_part_ = nullptr, *d_amax_val_ = nullptr, *d_gemm_ws_ = nullptr;
     int *d_amax_idx_ = nullptr;
     ActQ8 act0_, actk_;  // Q8_0 and Q8_K batches
+    ActQ8 act_h_;        // Q8_0 of the single-token FFN hidden
     size_t kmax_ = 0, ff_max_ = 0, part_floats_ = 0;
     // MoE scratch
     float *d_router_ = nullptr, *d_moe_w_ = nullptr, *d_moe_h_ = nullptr, *d_moe_y_ = nullptr;

@@ -25,8 +25,10 @@ struct GemvSeg {
 // Returns false when a weight type/shape has no kernel.
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st);
 // h = act(gate·x) ⊙ (up·x) for gated feed-forward blocks (gelu selects GELU-tanh).
+// hq (n_tok == 1, Q8_0 down projection): also quantize h to Q8_0 in the epilogue;
+// returns false (nothing launched) when that is not possible.
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
-                     int ld, int gelu, hipStream_t st);
+                     int ld, int gelu, const ActQ8 *hq, hipStream_t st);
 bool gemv_supported(int ty, size_t K);
 
 // ---- attention.hip ----

@@ -271,15 +271,20 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    // V accumulators: thread owns (head j, dims) pairs
-    const int n_out = G * hd;
-    constexpr int MAXO = MAXG * 256 / 256;  // outputs per thread upper bound
-    float o_acc[MAXO];
+    // V accumulation: an item is (head j, 8-dim chunk c); NI items, P groups of
+    // positions; each thread owns one (item, group) and 8 accumulators.
+    const int NI = G * (hd / 8);
+    const int P = max(1, 256 / NI);
+    const int item = tid % NI, pg = tid / NI;
+    const bool v_active = tid < NI * P;
+    const int vj = item / (hd / 8), vc = item % (hd / 8);
+    float o8[8];
 #pragma unroll
-    for (int i = 0; i < MAXO; i++) o_acc[i] = 0.0f;
+    for (int i = 0; i < 8; i++) o8[i] = 0.0f;
 
     const size_t kv_row0 = (size_t)g * a.slots;
     const size_t q8rb = (size_t)(hd / 32) * 34;
+    const int tb = turbo_block(hd);
     for (int tile = r0; tile < r1; tile += ATT_TILE) {
         const int nt = min(ATT_TILE, r1 - tile);
         // ---- scores, one lane per position ----
@@ -311,24 +316,28 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
                 for (int bi = 0; bi < hd / 32; bi++) {
                     const uint8_t *blk = kr + bi * 34;
                     const float dk = h2f(blk[0] | (blk[1] << 8));
+                    int8_t kq[32];
+#pragma unroll
+                    for (int i = 0; i < 32; i++) kq[i] = (int8_t)blk[2 + i];
                     for (int j = 0; j < G; j++) {
                         const int8_t *qq = qs_i + j * hd + bi * 32;
                         int acc = 0;
-                        for (int i = 0; i < 32; i++) acc += (int)(int8_t)blk[2 + i] * qq[i];
+#pragma unroll
+                        for (int i = 0; i < 32; i++) acc += (int)kq[i] * qq[i];
                         sj[j] = fmaf(dk * qs_d[(j * hd) / 32 + bi], (float)acc, sj[j]);
                     }
                 }
             } else {
                 const uint8_t *kr = a.k_cache + row * (size_t)(hd / 2);
-                const int b = turbo_block(hd);
                 for (int bi = 0; bi < hd / 32; bi++) {
                     int8_t lv[32];
                     turbo_levels32(kr + bi * 16, lv);
+                    const float ks = h2f(a.k_scale[row * (hd / tb) + (bi * 32) / tb]);
                     for (int j = 0; j < G; j++) {
                         const int8_t *qq = qs_i + j * hd + bi * 32;
                         int acc = 0;
+#pragma unroll
                         for (int i = 0; i < 32; i++) acc += (int)lv[i] * qq[i];
-                        const float ks = h2f(a.k_scale[row * (hd / b) + (bi * 32) / b]);
                         sj[j] = fmaf(qs_d[(j * hd) / 32 + bi] * ks * (1.0f / 46.0f), (float)acc, sj[j]);
                     }
                 }
@@ -362,39 +371,56 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        // ---- V accumulation: thread owns outputs o = tid + 256·i ----
-        for (int i = 0; i < MAXO; i++) {
-            const int oi = tid + 256 * i;
-            if (oi >= n_out) break;
-            const int j = oi / hd, d = oi % hd;
-            float acc = o_acc[i] * alpha[j];
-            for (int pi = 0; pi < nt; pi++) {
+        // ---- V accumulation: 16-byte V-row loads per (item, position) ----
+        if (v_active) {
+            const float al = alpha[vj];
+#pragma unroll
+            for (int i = 0; i < 8; i++) o8[i] *= al;
+            for (int pi = pg; pi < nt; pi += P) {
                 const size_t row = kv_row0 + (tile + pi) % a.slots;
-                float vv;
+                const float pw = sc[vj][pi];
+                float vv[8];
                 if (a.kv_type == 0) {
-                    vv = h2f(((const uint16_t *)a.v_cache)[row * hd + d]);
+                    const uint4 w4 = *(const uint4 *)(a.v_cache + (row * hd + vc * 8) * 2);
+                    const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        vv[2 * i] = h2f(ww[i] & 0xffff);
+                        vv[2 * i + 1] = h2f(ww[i] >> 16);
+                    }
                 } else if (a.kv_type == 1) {
-                    const uint8_t *blk = a.v_cache + row * q8rb + (d / 32) * 34;
-                    vv = h2f(blk[0] | (blk[1] << 8)) * (float)(int8_t)blk[2 + (d & 31)];
+                    const uint8_t *blk = a.v_cache + row * q8rb + (vc * 8 / 32) * 34;
+                    const float dv = h2f(blk[0] | (blk[1] << 8));
+#pragma unroll
+                    for (int i = 0; i < 8; i++) vv[i] = dv * (float)(int8_t)blk[2 + (vc * 8) % 32 + i];
                 } else {
-                    const int b = turbo_block(hd);
-                    const uint8_t cb = a.v_cache[row * (size_t)(hd / 2) + (d / 32) * 16 + (d & 15)];
-                    const int code = (d & 31) < 16 ? (cb & 15) : (cb >> 4);
-                    vv = h2f(a.v_scale[row * (hd / b) + d / b]) * (1.0f / 46.0f) * (float)KV_LEVELS_I8[code];
+                    const int d0 = vc * 8;
+                    const uint8_t *cb = a.v_cache + row * (size_t)(hd / 2) + (d0 / 32) * 16 + (d0 % 16);
+                    const bool hi = (d0 % 32) >= 16;
+                    const float vs = h2f(a.v_scale[row * (hd / tb) + d0 / tb]) * (1.0f / 46.0f);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) vv[i] = vs * (float)KV_LEVELS_I8[hi ? (cb[i] >> 4) : (cb[i] & 15)];
                 }
-                acc = fmaf(sc[j][pi], vv, acc);
+#pragma unroll
+                for (int i = 0; i < 8; i++) o8[i] = fmaf(pw, vv[i], o8[i]);
             }
-            o_acc[i] = acc;
         }
         __syncthreads();
     }
-    // ---- partial result of this range ----
+    // ---- reduce the position groups, write this range's partial ----
+    float *red = &sc[0][0];  // reuse the score tile: P·NI·8 ≤ 8·256 floats
+    if (v_active && pg > 0)
+#pragma unroll
+        for (int i = 0; i < 8; i++) red[((pg - 1) * NI + item) * 8 + i] = o8[i];
+    __syncthreads();
     float *part = a.part + (((size_t)t * a.n_head + (size_t)g * G) * a.n_split) * (hd + 2);
-    for (int i = 0; i < MAXO; i++) {
-        const int oi = tid + 256 * i;
-        if (oi >= n_out) break;
-        const int j = oi / hd, d = oi % hd;
-        part[((size_t)j * a.n_split + s_idx) * (hd + 2) + d] = o_acc[i];
+    if (v_active && pg == 0) {
+        for (int q = 1; q < P; q++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) o8[i] += red[((q - 1) * NI + item) * 8 + i];
+        float *dst = part + ((size_t)vj * a.n_split + s_idx) * (hd + 2) + vc * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dst[i] = o8[i];
     }
     if (tid < G) {
         float *pp = part + ((size_t)tid * a.n_split + s_idx) * (hd + 2);

@@ -18,10 +18,27 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace rie {
 
 constexpr int MAXT = 4;  // tokens processed per weight load
 constexpr uint32_t M4 = 0x0F0F0F0Fu;
+
+// 6-bit scale and min j (0..7) of a Q4_K superblock from its 12 packed bytes
+// (h1,h2,h3 little-endian), get_scale_min_k4 (crates/rie-core/src/quant/reference.rs:8-16).
+__device__ __forceinline__ void q4k_scale_min(uint32_t h1, uint32_t h2, uint32_t h3, int j, int &sc, int &mn) {
+    const int sh = 8 * (j & 3);
+    const uint32_t b1 = (h1 >> sh) & 0xff, b2 = (h2 >> sh) & 0xff, b3 = (h3 >> sh) & 0xff;
+    if (j < 4) {
+        sc = b1 & 63;
+        mn = b2 & 63;
+    } else {
+        sc = (b3 & 0xF) | ((b1 >> 6) << 4);
+        mn = (b3 >> 4) | ((b2 >> 6) << 4);
+    }
+}
 
 struct SegP {
     const uint8_t *w;
@@ -116,23 +133,9 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
         const u32x4 v0 = ld_nt16(b + 16 + 32 * qi);
         const u32x4 v1 = ld_nt16(b + 32 + 32 * qi);
         const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
-        uint8_t s[12];
-        const uint32_t h1 = hdr.y, h2 = hdr.z, h3 = hdr.w;
-        __builtin_memcpy(s, &h1, 4);
-        __builtin_memcpy(s + 4, &h2, 4);
-        __builtin_memcpy(s + 8, &h3, 4);
         int sc[2], mn[2];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int j = 2 * qi + h;
-            if (j < 4) {
-                sc[h] = s[j] & 63;
-                mn[h] = s[j + 4] & 63;
-            } else {
-                sc[h] = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
-                mn[h] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-            }
-        }
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi, sc[0], mn[0]);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi + 1, sc[1], mn[1]);
         const uint32_t v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         const int nsb = K >> 8;
 #pragma unroll
@@ -270,6 +273,365 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvP p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Single-token decode GEMV.  A workgroup owns TR consecutive rows; LPR lanes
+// (16..256) share a row so that each lane holds UPL ≤ 2 units.  The lane's
+// activation slice is loaded into registers once and reused for every row of
+// the workgroup; per-lane partial sums go to a padded LDS tile
+// [row][LPR+1] (conflict-free column reads) and one thread per row adds them.
+// GLU: gate and up rows give h = act(g)·u, optionally quantized to Q8_0 in the
+// epilogue (32 rows per half-wave) for the down projection.
+// ---------------------------------------------------------------------------
+struct DecP {
+    SegP seg[3];
+    int nseg, total_rows, K;
+    int tr;          // rows per workgroup
+    ActQ8 act;
+    const float *actf;
+    int glu;         // 0 none, 1 silu, 2 gelu
+    ActQ8 hq;        // GLU: Q8_0 output of h when hq.qs != nullptr
+};
+
+template <int TY>
+struct ActSlice {
+    uint32_t q[16];
+    float d0, d1;
+    int i0, i1;
+    int16_t bs[4];
+    float f[8];
+};
+
+template <int TY>
+__device__ __forceinline__ void load_act(ActSlice<TY> &a, int u, const ActQ8 &act, const float *actf, int K) {
+    if constexpr (TY == T_Q4_0 || TY == T_Q8_0) {
+        const uint4 *ap = (const uint4 *)(act.qs + 64 * u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = ap[i];
+            a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+        }
+        a.d0 = act.d[2 * u];
+        a.d1 = act.d[2 * u + 1];
+        if constexpr (TY == T_Q4_0) {
+            a.i0 = act.isum[2 * u];
+            a.i1 = act.isum[2 * u + 1];
+        }
+    } else if constexpr (TY == T_Q4_K) {
+        const int sb = u >> 2, qi = u & 3;
+        const uint4 *ap = (const uint4 *)(act.qs + 256 * sb + 64 * qi);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = ap[i];
+            a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+        }
+        a.d0 = act.d[sb];
+#pragma unroll
+        for (int i = 0; i < 4; i++) a.bs[i] = act.bsums[16 * sb + 4 * qi + i];
+    } else if constexpr (TY == T_Q6_K) {
+        const int sb = u >> 3, r = u & 7, n = r >> 2, k = r & 3;
+        const uint4 *ap = (const uint4 *)(act.qs + 256 * sb + 128 * n + 32 * k);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint4 v = ap[i];
+            a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+        }
+        a.d0 = act.d[sb];
+        a.bs[0] = act.bsums[16 * sb + 8 * n + 2 * k];
+        a.bs[1] = act.bsums[16 * sb + 8 * n + 2 * k + 1];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) a.f[i] = actf[8 * u + i];
+    }
+}
+
+template <int TY>
+__device__ __forceinline__ float dec_unit(const uint8_t *__restrict__ row, int u, const ActSlice<TY> &a) {
+    if constexpr (TY == T_Q4_0) {
+        const uint32_t *wp = (const uint32_t *)(row + 36 * u);
+        uint32_t w[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) w[i] = __builtin_nontemporal_load(wp + i);
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[4 + i] = w[5 + i];
+        int i0 = 0, i1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            i0 = sdot4(q[i] & M4, a.q[i], i0);
+            i0 = sdot4((q[i] >> 4) & M4, a.q[4 + i], i0);
+            i1 = sdot4(q[4 + i] & M4, a.q[8 + i], i1);
+            i1 = sdot4((q[4 + i] >> 4) & M4, a.q[12 + i], i1);
+        }
+        i0 -= 8 * a.i0;
+        i1 -= 8 * a.i1;
+        const float r0 = h2f(w[0] & 0xffff) * a.d0 * (float)i0;
+        return fmaf(h2f(w[4] >> 16) * a.d1, (float)i1, r0);
+    } else if constexpr (TY == T_Q8_0) {
+        const uint32_t *wp = (const uint32_t *)(row + 68 * u);
+        uint32_t w[17];
+#pragma unroll
+        for (int i = 0; i < 17; i++) w[i] = __builtin_nontemporal_load(wp + i);
+        int i0 = 0, i1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) i0 = sdot4(__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2), a.q[i], i0);
+#pragma unroll
+        for (int i = 0; i < 8; i++) i1 = sdot4(w[9 + i], a.q[8 + i], i1);
+        const float r0 = h2f(w[0] & 0xffff) * a.d0 * (float)i0;
+        return fmaf(h2f(w[8] >> 16) * a.d1, (float)i1, r0);
+    } else if constexpr (TY == T_Q4_K) {
+        const int sb = u >> 2, qi = u & 3;
+        const uint8_t *b = row + 144 * sb;
+        const u32x4 hdr = ld_nt16(b);
+        const u32x4 v0 = ld_nt16(b + 16 + 32 * qi);
+        const u32x4 v1 = ld_nt16(b + 32 + 32 * qi);
+        int sc[2], mn[2];
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi, sc[0], mn[0]);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi + 1, sc[1], mn[1]);
+        const uint32_t v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        int s1 = 0, s2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s1 = sdot4(v[i] & M4, a.q[i], s1);
+            s2 = sdot4((v[i] >> 4) & M4, a.q[8 + i], s2);
+        }
+        const int sumi = s1 * sc[0] + s2 * sc[1];
+        const int summ = mn[0] * ((int)a.bs[0] + a.bs[1]) + mn[1] * ((int)a.bs[2] + a.bs[3]);
+        return (h2f(hdr.x & 0xffff) * a.d0) * (float)sumi - (h2f(hdr.x >> 16) * a.d0) * (float)summ;
+    } else if constexpr (TY == T_Q6_K) {
+        const int sb = u >> 3, r = u & 7, n = r >> 2, k = r & 3;
+        const uint8_t *b = row + 210 * sb;
+        uint32_t ql[8], qh[8];
+        load32_a2(b + 64 * n + 32 * (k & 1), ql);
+        load32_a2(b + 128 + 32 * n, qh);
+        const uint16_t scw = *(const uint16_t *)(b + 192 + 8 * n + 2 * k);
+        const int sh = k >= 2 ? 4 : 0, hs = 2 * k;
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t v = ((ql[j] >> sh) & M4) | (((qh[j] >> hs) & 0x03030303u) << 4);
+            if (j < 4) dl = sdot4(v, a.q[j], dl);
+            else dh = sdot4(v, a.q[j], dh);
+        }
+        const int sumi = (int)(int8_t)(scw & 0xff) * (dl - 32 * a.bs[0]) + (int)(int8_t)(scw >> 8) * (dh - 32 * a.bs[1]);
+        return h2f(*(const uint16_t *)(b + 208)) * a.d0 * (float)sumi;
+    } else if constexpr (TY == T_F32) {
+        const f32x4 w0 = ld_nt16f(row + 32 * u), w1 = ld_nt16f(row + 32 * u + 16);
+        float s = 0.0f;
+        s = fmaf(w0.x, a.f[0], s); s = fmaf(w0.y, a.f[1], s); s = fmaf(w0.z, a.f[2], s); s = fmaf(w0.w, a.f[3], s);
+        s = fmaf(w1.x, a.f[4], s); s = fmaf(w1.y, a.f[5], s); s = fmaf(w1.z, a.f[6], s); s = fmaf(w1.w, a.f[7], s);
+        return s;
+    } else {
+        const u32x4 wv = ld_nt16(row + 16 * u);
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s = fmaf(h2f(wd[i] & 0xffff), a.f[2 * i], s);
+            s = fmaf(h2f(wd[i] >> 16), a.f[2 * i + 1], s);
+        }
+        return s;
+    }
+}
+
+template <int TY>
+constexpr int dec_rows_per_pass() { return (TY == T_Q8_0 || TY == T_Q6_K || TY == T_F32) ? 2 : 4; }
+
+// Row pointer of (clamped) row r: the segments are stacked in row order
+// (GLU: gate rows only; the matching up row has the same index in seg[1]).
+__device__ __forceinline__ const uint8_t *dec_row(const DecP &p, int r) {
+    int rr = r;
+    const uint8_t *w = p.seg[0].w;
+    size_t rb = p.seg[0].rb;
+    if (!p.glu && p.nseg > 1 && rr >= p.seg[0].rows) {
+        rr -= p.seg[0].rows;
+        if (p.nseg > 2 && rr >= p.seg[1].rows) {
+            rr -= p.seg[1].rows;
+            w = p.seg[2].w;
+            rb = p.seg[2].rb;
+        } else {
+            w = p.seg[1].w;
+            rb = p.seg[1].rb;
+        }
+    }
+    return w + (size_t)rr * rb;
+}
+
+constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
+
+template <int TY, int LPR, int UPL>
+__global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
+    constexpr int GROUPS = 256 / LPR;
+    constexpr int R = dec_rows_per_pass<TY>();
+    constexpr int STRIDE = LPR + DEC_PAD;
+    extern __shared__ float red[];  // [glu ? 2 : 1][tr][STRIDE], then tr floats of h
+    const int tid = threadIdx.x;
+    const int grp = tid / LPR, l = tid % LPR;
+    const int U = units_per_row<TY>(p.K);
+    ActSlice<TY> a[UPL];
+#pragma unroll
+    for (int k = 0; k < UPL; k++)
+        if (l + LPR * k < U) load_act<TY>(a[k], l + LPR * k, p.act, p.actf, p.K);
+    const int row0 = blockIdx.x * p.tr;
+    const int last = p.total_rows - 1;
+    // R rows per pass: the loads of all R rows are issued before their dots
+    for (int base = grp * R; base < p.tr; base += GROUPS * R) {
+        float acc[R], acc2[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            const int r = min(row0 + base + k, last);
+            const uint8_t *row = dec_row(p, r);
+            float s = 0.0f;
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (l + LPR * u < U) s += dec_unit<TY>(row, l + LPR * u, a[u]);
+            acc[k] = s;
+            if (p.glu) {
+                const uint8_t *row2 = p.seg[1].w + (size_t)r * p.seg[1].rb;
+                float s2 = 0.0f;
+#pragma unroll
+                for (int u = 0; u < UPL; u++)
+                    if (l + LPR * u < U) s2 += dec_unit<TY>(row2, l + LPR * u, a[u]);
+                acc2[k] = s2;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            red[(base + k) * STRIDE + l] = acc[k];
+            if (p.glu) red[(p.tr + base + k) * STRIDE + l] = acc2[k];
+        }
+    }
+    __syncthreads();
+    // 8 threads per row add its LPR partials
+    float *hv = red + (p.glu ? 2 : 1) * p.tr * STRIDE;
+    const int s8 = tid & 7;
+    for (int i = tid >> 3; i < ((p.tr + 31) & ~31); i += 32) {
+        float sum = 0.0f, sum2 = 0.0f;
+        if (i < p.tr) {
+            for (int j = s8; j < LPR; j += 8) sum += red[i * STRIDE + j];
+            if (p.glu)
+                for (int j = s8; j < LPR; j += 8) sum2 += red[(p.tr + i) * STRIDE + j];
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            sum += __shfl_xor(sum, o, 64);
+            sum2 += __shfl_xor(sum2, o, 64);
+        }
+        const int r = row0 + i;
+        if (s8 == 0 && i < p.tr && r < p.total_rows) {
+            float v = sum;
+            if (p.glu) v = (p.glu == 2 ? gelu_tanh_f(sum) : silu_f(sum)) * sum2;
+            int rr = r;
+            float *out = p.seg[0].out;
+            int epi = p.seg[0].epi;
+            if (!p.glu && p.nseg > 1 && rr >= p.seg[0].rows) {
+                rr -= p.seg[0].rows;
+                if (p.nseg > 2 && rr >= p.seg[1].rows) {
+                    rr -= p.seg[1].rows;
+                    out = p.seg[2].out;
+                    epi = p.seg[2].epi;
+                } else {
+                    out = p.seg[1].out;
+                    epi = p.seg[1].epi;
+                }
+            }
+            if (epi == EPI_ADD) out[rr] += v;
+            else out[rr] = v;
+            hv[i] = v;
+        }
+    }
+    if (!(p.glu && p.hq.qs)) return;
+    // Q8_0 of h (ops: avx2 quantizer semantics), one half-wave per 32 rows
+    __syncthreads();
+    if (tid < p.tr) {
+        const int r = row0 + tid;
+        const float y = r < p.total_rows ? hv[tid] : 0.0f;
+        float amax = fabsf(y);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q = (int)rintf(y * id);
+        const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
+        int su = q, scl = qc;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            su += __shfl_xor(su, o, 64);
+            scl += __shfl_xor(scl, o, 64);
+        }
+        if (r < p.total_rows) {
+            p.hq.qs[r] = (int8_t)qc;
+            if ((r & 31) == 0) {
+                p.hq.d[r >> 5] = d;
+                if (p.hq.s) p.hq.s[r >> 5] = d * (float)su;
+                if (p.hq.isum) p.hq.isum[r >> 5] = scl;
+            }
+        }
+    }
+}
+
+static int dec_units(int ty, int K) { return ty == T_Q6_K ? K / 32 : (ty == T_F32 || ty == T_F16) ? K / 8 : K / 64; }
+
+// Rows-per-workgroup multiplier override (0 = automatic), for launch-shape sweeps.
+static int dec_tile_override() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RIE_HIP_GEMV_TILE");
+        v = e ? atoi(e) : 0;
+    }
+    return v;
+}
+
+template <int TY>
+static bool launch_dec_t(DecP p, hipStream_t st) {
+    constexpr int R = dec_rows_per_pass<TY>();
+    const int U = dec_units(TY, p.K);
+    int lpr = 16;
+    while (lpr < U && lpr < 256) lpr *= 2;
+    const int upl = (U + lpr - 1) / lpr;
+    if (upl > 2) return false;
+    const int pass = (256 / lpr) * R;  // rows per pass of the workgroup
+    int m;
+    if (p.glu && p.hq.qs) {
+        if (p.total_rows % 32) return false;
+        m = pass >= 32 ? 1 : 32 / pass;  // whole Q8_0 blocks of h per workgroup
+    } else {
+        const int ov = dec_tile_override();
+        m = ov > 0 ? ov : std::max(1, std::min(4, p.total_rows / (pass * 1024)));
+    }
+    p.tr = pass * m;
+    const size_t lds = ((size_t)(p.glu ? 2 : 1) * p.tr * (lpr + DEC_PAD) + p.tr) * sizeof(float);
+    if (lds > 64 * 1024) return false;
+    const int blocks = (p.total_rows + p.tr - 1) / p.tr;
+#define RIE_DEC(L, UP) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP>), dim3(blocks), dim3(256), lds, st, p)
+    if (upl == 1) {
+        switch (lpr) {
+        case 16: RIE_DEC(16, 1); break;
+        case 32: RIE_DEC(32, 1); break;
+        case 64: RIE_DEC(64, 1); break;
+        case 128: RIE_DEC(128, 1); break;
+        default: RIE_DEC(256, 1); break;
+        }
+    } else {
+        RIE_DEC(256, 2);
+    }
+#undef RIE_DEC
+    return true;
+}
+
+static bool dispatch_dec(int ty, const DecP &p, hipStream_t st) {
+    switch (ty) {
+    case T_Q4_0: return launch_dec_t<T_Q4_0>(p, st);
+    case T_Q8_0: return launch_dec_t<T_Q8_0>(p, st);
+    case T_Q4_K: return launch_dec_t<T_Q4_K>(p, st);
+    case T_Q6_K: return launch_dec_t<T_Q6_K>(p, st);
+    case T_F32: return launch_dec_t<T_F32>(p, st);
+    case T_F16: return launch_dec_t<T_F16>(p, st);
+    default: return false;
+    }
+}
+
 bool gemv_supported(int ty, size_t K) {
     switch (ty) {
     case T_Q4_0: case T_Q8_0: return K % 64 == 0;
@@ -342,14 +704,25 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
         p.n_tok = n_tok;
         p.K = K;
         p.glu = 0;
-        if (!dispatch(segs[i].w.ty, p, st)) return false;
+        bool done = false;
+        if (n_tok == 1) {
+            DecP d{};
+            for (int s = 0; s < p.nseg; s++) d.seg[s] = p.seg[s];
+            d.nseg = p.nseg;
+            d.total_rows = p.total_rows;
+            d.K = K;
+            d.act = act;
+            d.actf = act_f32;
+            done = dispatch_dec(segs[i].w.ty, d, st);
+        }
+        if (!done && !dispatch(segs[i].w.ty, p, st)) return false;
         i = j;
     }
     return true;
 }
 
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
-                     int ld, int gelu, hipStream_t st) {
+                     int ld, int gelu, const ActQ8 *hq, hipStream_t st) {
     if (gate.ty != up.ty || gate.rows != up.rows || !gemv_supported(gate.ty, K) || gate.cols != (size_t)K || up.cols != (size_t)K ||
         !gate.data || !up.data || !h || n_tok < 1 || !operands_ok(gate.ty, act, act_f32))
         return false;
@@ -363,6 +736,20 @@ bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
     p.n_tok = n_tok;
     p.K = K;
     p.glu = gelu ? 2 : 1;
+    if (n_tok == 1) {
+        DecP d{};
+        d.seg[0] = p.seg[0];
+        d.seg[1] = p.seg[1];
+        d.nseg = 2;
+        d.total_rows = p.total_rows;
+        d.K = K;
+        d.act = act;
+        d.actf = act_f32;
+        d.glu = p.glu;
+        if (hq) d.hq = *hq;
+        if (dispatch_dec(gate.ty, d, st)) return true;
+    }
+    if (hq) return false;  // the batched kernel does not quantize h
     return dispatch(gate.ty, p, st);
 }
 

@@ -15,10 +15,16 @@
 
 namespace rie {
 
+// Grid (row chunks, rows): every workgroup recomputes its row's sum of squares
+// (the row is L2-resident) and quantizes QB8 blocks of 32 (Q8_0: 8 per
+// iteration, one per half-wave) or 4 blocks of 256 (Q8_K: one per wave).
+constexpr int Q8_0_BLOCKS_PER_WG = 16;
+constexpr int Q8K_BLOCKS_PER_WG = 4;
+
 template <int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w,
                                                             float eps, int E, float *__restrict__ xn, ActQ8 act) {
-    const int row = blockIdx.x;
+    const int row = blockIdx.y;
     const int tid = threadIdx.x;
     const float *xr = x + (size_t)row * ldx;
     __shared__ float red[4];
@@ -26,7 +32,13 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
     float scale = 1.0f;
     if (w) {
         float ss = 0.0f;
-        for (int i = tid; i < E; i += 256) ss = fmaf(xr[i], xr[i], ss);
+        for (int i = tid * 4; i < E; i += 1024) {
+            const float4 v = *(const float4 *)(xr + i);
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
         ss = wave_sum(ss, 64);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
@@ -40,7 +52,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
     if (FMT == ACT_Q8_0) {
         const int hw = tid >> 5, j = tid & 31;
         const int nb = E >> 5;
-        for (int b = hw; b < nb; b += 8) {
+        const int b0 = blockIdx.x * Q8_0_BLOCKS_PER_WG;
+        for (int b = b0 + hw; b < min(nb, b0 + Q8_0_BLOCKS_PER_WG); b += 8) {
             const int i = (b << 5) + j;
             float y = w ? xr[i] * scale * w[i] : xr[i];
             if (xn) xn[(size_t)row * E + i] = y;
@@ -68,7 +81,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
     } else {
         const int wv = tid >> 6, l = tid & 63;
         const int nb = E >> 8;
-        for (int b = wv; b < nb; b += 4) {
+        const int b = blockIdx.x * Q8K_BLOCKS_PER_WG + wv;
+        if (b < nb) {
             const int i0 = (b << 8) + (l << 2);
             float y[4];
 #pragma unroll
@@ -102,31 +116,34 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
                 for (int e = 0; e < 4; e++) qo[e] = 0;
                 if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = 0;
                 if (l == 0) act.d[bi] = 0.0f;
-                continue;
-            }
-            const float iscale = -127.0f / mx;
-            int s4 = 0;
+            } else {
+                const float iscale = -127.0f / mx;
+                int s4 = 0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                int q = (int)roundf(iscale * y[e]);
-                q = q < -127 ? -127 : (q > 127 ? 127 : q);
-                qo[e] = (int8_t)q;
-                s4 += q;
+                for (int e = 0; e < 4; e++) {
+                    int q = (int)roundf(iscale * y[e]);
+                    q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                    qo[e] = (int8_t)q;
+                    s4 += q;
+                }
+                s4 += __shfl_xor(s4, 1, 64);
+                s4 += __shfl_xor(s4, 2, 64);
+                if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = (int16_t)s4;
+                if (l == 0) act.d[bi] = 1.0f / iscale;
             }
-            s4 += __shfl_xor(s4, 1, 64);
-            s4 += __shfl_xor(s4, 2, 64);
-            if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = (int16_t)s4;
-            if (l == 0) act.d[bi] = 1.0f / iscale;
         }
     }
 }
 
 void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
                           hipStream_t st) {
-    if (fmt == ACT_Q8_0)
-        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
-    else
-        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8K>, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+    if (fmt == ACT_Q8_0) {
+        const int chunks = (E / 32 + Q8_0_BLOCKS_PER_WG - 1) / Q8_0_BLOCKS_PER_WG;
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+    } else {
+        const int chunks = (E / 256 + Q8K_BLOCKS_PER_WG - 1) / Q8K_BLOCKS_PER_WG;
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8K>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+    }
 }
 
 // RMSNorm without quantization (f32 out), one row per workgroup: ops.rs:7-14

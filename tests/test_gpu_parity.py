@@ -251,14 +251,52 @@ def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
                         assert np.array_equal(rows[h, t], ref[2:]) and scales[h, t] == ref[:2].view(np.uint16)[0]
 
 
-def test_greedy_sequence_matches_oracle_128_steps(oracle, cuda):
-    spec, g, o = _pair(oracle, "llama", Q4_0, 0, n_ctx=256, max_batch=16)
-    prompt = [(i * 7919 + 13) % spec.n_vocab for i in range(16)]
-    want, margins, _ = o.greedy(prompt, 128)
-    got = R.Engine(g).greedy(prompt, 128)
-    if not np.array_equal(got, want):
-        i = int(np.argmax(got != want))
-        pytest.fail(f"greedy diverges at step {i}: gpu {got[i]} cpu {want[i]}, cpu top-2 margin {margins[i]:.3g}")
+def _top2_margin(x):
+    a = np.partition(x, -2)[-2:]
+    return float(a[1] - a[0])
+
+
+def greedy_agreement(g, o, prompt, n_steps, nv):
+    """Teacher-forced greedy comparison: both backends are fed the CPU's choice
+    each step.  Returns per-step (gpu argmax, cpu argmax, cpu top-2 margin,
+    max |Δlogit|)."""
+    lg, lo = g.forward(prompt, 0), o.forward(prompt, 0)
+    rows = []
+    for step in range(n_steps):
+        ag, ac = R.argmax(lg), int(oracle_argmax(lo))
+        rows.append((ag, ac, _top2_margin(lo), float(np.abs(lg - lo).max())))
+        pos = len(prompt) + step
+        lg, lo = g.forward([ac], pos), o.forward([ac], pos)
+    return rows
+
+
+def oracle_argmax(x):
+    import pyoracle
+    return pyoracle.argmax(x)
+
+
+def check_greedy(oracle, arch, ty, n_steps=128, n_prompt=16, n_ctx=256):
+    spec, g, o = _pair(oracle, arch, ty, 0, n_ctx=n_ctx, max_batch=16)
+    nv = spec.n_vocab
+    prompt = [(i * 7919 + 13) % nv for i in range(n_prompt)]
+    rows = greedy_agreement(g, o, prompt, n_steps, nv)
+    bad = [(i, r) for i, r in enumerate(rows) if r[0] != r[1]]
+    noise = max(r[3] for r in rows)
+    print(f"{arch} {ty}: {n_steps - len(bad)}/{n_steps} teacher-forced greedy steps agree; max |dlogit| {noise:.3g}; "
+          f"disagreements (step, cpu margin, |dlogit|): {[(i, round(r[2], 5), round(r[3], 5)) for i, r in bad]}")
+    for i, r in bad:  # a disagreement is allowed only inside the numerical noise band
+        assert r[2] <= 2 * r[3], f"step {i}: cpu margin {r[2]} exceeds 2x logit difference {r[3]}"
+    # free-running device greedy follows the CPU sequence up to the first near-tie
+    first = bad[0][0] if bad else n_steps
+    want, _, _ = oracle.Backend(oracle.Model(synth.build(spec)), n_ctx, 16, 0, n_threads=4).greedy(prompt, n_steps)
+    got = R.Engine(R.HipBackend(synth.build(spec), n_ctx=n_ctx, max_batch=16)).greedy(prompt, n_steps)
+    assert np.array_equal(got[:first], want[:first])
+    return len(bad)
+
+
+def test_greedy_128_steps_match_oracle_outside_near_ties(oracle, cuda):
+    check_greedy(oracle, "llama", Q4_0)
+    check_greedy(oracle, "qwen3", Q4_K)
 
 
 def test_graph_replay_equals_eager(oracle, cuda):
