@@ -203,7 +203,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     actk_.qs = dalloc<int8_t>(allocs_, kq);
     actk_.d = dalloc<float>(allocs_, kq / 256 + 1);
     actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
-    part_floats_ = (size_t)32 * mb * c.n_head * (hd + 2);
+    part_floats_ = (size_t)std::max<size_t>(32 * mb, ATT_MAX_SPLIT) * c.n_head * (hd + 2);
     d_part_ = dalloc<float>(allocs_, part_floats_);
     d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
@@ -218,8 +218,10 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
 
 HipBackend::~HipBackend() {
     if (st_) (void)hipStreamSynchronize(st_);
-    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-    if (graph_) (void)hipGraphDestroy(graph_);
+    for (auto &kv : graphs_) {
+        (void)hipGraphExecDestroy(kv.second.exec);
+        (void)hipGraphDestroy(kv.second.graph);
+    }
     for (void *p : allocs_) (void)hipFree(p);
     if (d_blob_) (void)hipFree(d_blob_);
     if (st_) (void)hipStreamDestroy(st_);
@@ -278,14 +280,21 @@ void HipBackend::prepare(const float *x, const float *norm, int n, int K, const 
 // matmul_multi (matmul.rs:136-176): decode-sized batches stream the weights
 // through the GEMV kernels; prompt batches go to the int8 MFMA GEMM.
 void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0) {
-    // group by activation format: each launch reads one activation batch
-    for (int i = 0; i < nseg; i++) {
+    // runs of segments that read the same activation batch share one launch
+    int i = 0;
+    while (i < nseg) {
         const int fmt = act_format(segs[i].w.ty);
+        int j = i + 1;
+        while (j < nseg && act_format(segs[j].w.ty) == fmt) j++;
         const ActQ8 &a = fmt == ACT_Q8K ? actk_ : (act_q8_0 ? *act_q8_0 : act0_);
-        bool done = false;
-        if (n > 8 && gemm_supported(segs[i].w.ty, K)) done = launch_gemm(&segs[i], 1, a, n, K, st_);
-        if (!done && !launch_gemv(&segs[i], 1, a, d_xn_, n, K, st_))
-            throw Error{E_UNSUPPORTED, std::string("unsupported: matmul of type ") + type_name(segs[i].w.ty)};
+        for (int s = i; s < j; s++) {
+            bool done = false;
+            if (n > 8 && gemm_supported(segs[s].w.ty, K)) done = launch_gemm(&segs[s], 1, a, n, K, st_);
+            if (!done && !launch_gemv(&segs[s], (n > 8) ? 1 : j - s, a, d_xn_, n, K, st_))
+                throw Error{E_UNSUPPORTED, std::string("unsupported: matmul of type ") + type_name(segs[s].w.ty)};
+            if (!done && n <= 8) break;  // the single-token/small-batch launch took the whole run
+        }
+        i = j;
     }
     check_launch("matmul");
 }
@@ -484,7 +493,7 @@ void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_
     if (n == 1 && use_graph_ && !capture_) {
         decode_step_graph(pos);
     } else {
-        run_layers((int)n, pos, nullptr, all_logits, decode_split());
+        run_layers((int)n, pos, nullptr, all_logits, splits_for(n, pos));
     }
     RIE_HIP_CHECK(hipMemcpyAsync(logits, d_logits_, m * c.n_vocab * 4, hipMemcpyDeviceToHost, st_));
     RIE_HIP_CHECK(hipStreamSynchronize(st_));
@@ -492,17 +501,20 @@ void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_
 }
 
 // The decode step as a graph: kernels read pos from d_pos_ and the token from
-// d_tokens_[0]; the host only writes {pos} into pinned memory before a replay.
+// d_tokens_[0].  One graph per attention range count (it grows with the context).
 void HipBackend::decode_step_graph(size_t pos) {
     // the position travels as a kernel argument (copied at launch), so queued
     // steps never share a host-side slot
     launch_set_int(d_pos_, (int)pos, st_);
     check_launch("set pos");
-    if (!graph_exec_) {
+    const int ns = splits_for(1, pos);
+    auto it = graphs_.find(ns);
+    if (it == graphs_.end()) {
+        DecodeGraph dg;
         in_capture_ = true;
         RIE_HIP_CHECK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
         try {
-            run_layers(1, 0, d_pos_, false, decode_split());
+            run_layers(1, 0, d_pos_, false, ns);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(st_, &g);
@@ -510,11 +522,16 @@ void HipBackend::decode_step_graph(size_t pos) {
             in_capture_ = false;
             throw;
         }
-        RIE_HIP_CHECK(hipStreamEndCapture(st_, &graph_));
+        RIE_HIP_CHECK(hipStreamEndCapture(st_, &dg.graph));
         in_capture_ = false;
-        RIE_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+        RIE_HIP_CHECK(hipGraphInstantiate(&dg.exec, dg.graph, nullptr, nullptr, 0));
+        it = graphs_.emplace(ns, dg).first;
     }
-    RIE_HIP_CHECK(hipGraphLaunch(graph_exec_, st_));
+    RIE_HIP_CHECK(hipGraphLaunch(it->second.exec, st_));
+}
+
+int HipBackend::splits_for(size_t n, size_t pos) const {
+    return attention_splits((int)n, (int)m_.cfg.n_head_kv, (int)(pos + n));
 }
 
 const float *HipBackend::hidden(size_t *rows) {
@@ -539,7 +556,7 @@ uint32_t HipBackend::forward_argmax(const uint32_t *tokens, size_t n, size_t pos
     if (n == 1 && use_graph_ && !capture_) {
         decode_step_graph(pos);
     } else {
-        run_layers((int)n, pos, nullptr, false, decode_split());
+        run_layers((int)n, pos, nullptr, false, splits_for(n, pos));
     }
     launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
     check_launch("argmax");
@@ -562,7 +579,7 @@ void HipBackend::generate_greedy(size_t pos, size_t n_gen, uint32_t *out) {
         if (use_graph_ && !capture_) {
             decode_step_graph(pos + i);
         } else {
-            run_layers(1, pos + i, nullptr, false, decode_split());
+            run_layers(1, pos + i, nullptr, false, splits_for(1, pos + i));
         }
         launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
         check_launch("argmax");
@@ -621,7 +638,7 @@ std::vector<HipBackend::KernelTime> HipBackend::profile_decode(size_t pos, int r
         RIE_HIP_CHECK(hipEventCreate(&mark0_));
         RIE_HIP_CHECK(hipEventRecord(mark0_, st_));
         try {
-            run_layers(1, pos, nullptr, false, decode_split());
+            run_layers(1, pos, nullptr, false, splits_for(1, pos));
         } catch (...) {
             profiling_ = false;
             throw;

@@ -8,6 +8,7 @@
 
 #include <memory>
 #include <string>
+#include <map>
 #include <vector>
 
 namespace rie {
@@ -93,7 +94,7 @@ class HipBackend {
     void decode_step_graph(size_t pos);
     // context ranges per (token, kv head) in attention; the same for every batch size so
     // a token's attention does not depend on how its batch was formed
-    int decode_split() const { return 32; }
+    int splits_for(size_t n, size_t pos) const;  // attention context ranges of a launch
 
     HostModel m_;
     std::string name_;
@@ -139,8 +140,11 @@ class HipBackend {
     std::vector<std::pair<const char *, hipEvent_t>> marks_;
     hipEvent_t mark0_ = nullptr;
 
-    hipGraph_t graph_ = nullptr;
-    hipGraphExec_t graph_exec_ = nullptr;
+    struct DecodeGraph {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+    };
+    std::map<int, DecodeGraph> graphs_;  // by attention range count
     bool in_capture_ = false;
 };
 

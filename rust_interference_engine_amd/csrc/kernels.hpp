@@ -66,6 +66,9 @@ struct AttnArgs {
     const float *turbo_signs;
 };
 void launch_attention(const AttnArgs &a, hipStream_t st);
+// number of context ranges (n_split) for a launch whose longest query sees max_len positions
+constexpr int ATT_MAX_SPLIT = 256;
+int attention_splits(int n_tok, int n_kv, int max_len);
 
 // ---- misc.hip ----
 void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st);

@@ -22,6 +22,8 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <algorithm>
+
 namespace rie {
 
 __constant__ int8_t KV_LEVELS_I8[16] = {-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126};
@@ -191,20 +193,87 @@ void launch_head_prep(const HeadPrepArgs &a, hipStream_t st) {
 }
 
 // ---- attention over the cache ---------------------------------------------------
-constexpr int ATT_TILE = 256;
-constexpr int MAXG = 8;
+// A workgroup owns one (range, kv head, token).  SUB = hd/8 lanes (rounded up to
+// a power of two) share a cache position, each lane holding 8 dims (16 bytes of
+// an f16 row); PP = 256/SUB positions per pass, NP passes per tile, with the K
+// and V loads of the whole tile issued together.  Per-position scores are
+// reduced over the SUB lanes with DPP, the online softmax runs one wavefront per
+// query head, and each lane accumulates its 8 dims of V for every query head of
+// the group; the position slots are summed at the end.
+constexpr int ATT_NP = 4;
 
-__device__ __forceinline__ void turbo_levels32(const uint8_t *codes, int8_t out[32]) {
-    // 16 code bytes → 32 int8 levels in value order (low nibbles 0..15, high 16..31)
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint8_t c = codes[i];
-        out[i] = KV_LEVELS_I8[c & 15];
-        out[i + 16] = KV_LEVELS_I8[c >> 4];
+__device__ __forceinline__ float softcap_f(float v, float cap) { return cap > 0.0f ? cap * tanhf(v / cap) : v; }
+
+// 8 dims [d0, d0+8) of a row of the cache as floats (f16 / Q8_0 / Turbo4 levels·scale)
+template <int KVT>
+struct KvChunk {
+    uint4 raw;      // f16: 8 halves; Q8_0: 8 codes in x,y; Turbo4: 8 code bytes in x,y
+    uint32_t sc;    // Q8_0 block d or Turbo4 block scale (f16 bits)
+};
+
+template <int KVT>
+__device__ __forceinline__ void load_chunk(const uint8_t *cache, const uint16_t *scales, size_t row, int hd, int d0, int tb,
+                                           KvChunk<KVT> &c) {
+    if constexpr (KVT == 0) {
+        c.raw = *(const uint4 *)(cache + (row * hd + d0) * 2);
+        c.sc = 0;
+    } else if constexpr (KVT == 1) {
+        const uint8_t *blk = cache + row * (size_t)(hd / 32) * 34 + (d0 / 32) * 34;
+        const uint8_t *q = blk + 2 + (d0 % 32);
+        const uint32_t lo = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+        const uint32_t hi = (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
+        c.raw = make_uint4(lo, hi, 0, 0);
+        c.sc = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+    } else {
+        const uint2 v = *(const uint2 *)(cache + row * (size_t)(hd / 2) + (d0 / 32) * 16 + (d0 % 16));
+        c.raw = make_uint4(v.x, v.y, 0, 0);
+        c.sc = scales[row * (size_t)(hd / tb) + d0 / tb];
     }
 }
 
+// Turbo4: 8 codes of the chunk → 8 int8 levels packed in two dwords
+__device__ __forceinline__ void turbo_levels8(const KvChunk<2> &c, bool hi, uint32_t out[2]) {
+    const uint32_t w[2] = {c.raw.x, c.raw.y};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        uint32_t r = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t byte = (w[h] >> (8 * i)) & 0xff;
+            const uint32_t code = hi ? (byte >> 4) : (byte & 15);
+            r |= ((uint32_t)(uint8_t)KV_LEVELS_I8[code]) << (8 * i);
+        }
+        out[h] = r;
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ void chunk_values(const KvChunk<KVT> &c, int d0, float v[8]) {
+    if constexpr (KVT == 0) {
+        const uint32_t w[4] = {c.raw.x, c.raw.y, c.raw.z, c.raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[2 * i] = h2f(w[i] & 0xffff);
+            v[2 * i + 1] = h2f(w[i] >> 16);
+        }
+    } else if constexpr (KVT == 1) {
+        const float d = h2f(c.sc);
+        const uint32_t w[2] = {c.raw.x, c.raw.y};
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = d * (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xff);
+    } else {
+        const float s = h2f(c.sc) * (1.0f / 46.0f);
+        uint32_t lv[2];
+        turbo_levels8(c, (d0 % 32) >= 16, lv);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = s * (float)(int8_t)((lv[i >> 2] >> (8 * (i & 3))) & 0xff);
+    }
+}
+
+template <int KVT, int SUB, int MG>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+    constexpr int PP = 256 / SUB;  // position slots per pass
+    constexpr int TP = PP * ATT_NP;  // positions per tile
     const int s_idx = blockIdx.x, g = blockIdx.y, t = blockIdx.z;
     const int tid = threadIdx.x;
     const int hd = a.hd;
@@ -217,40 +286,42 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const int chunk = (len + a.n_split - 1) / a.n_split;
     const int r0 = start + s_idx * chunk;
     const int r1 = min(start + (s_idx + 1) * chunk, p + 1);
+    const int pi = tid / SUB, c = tid % SUB;
+    const bool cact = c < hd / 8;
+    const int d0 = cact ? 8 * c : 0;
+    const int tb = turbo_block(hd);
 
-    __shared__ float qs_f[MAXG * 256];       // query heads of the group (f32)
-    __shared__ int8_t qs_i[MAXG * 256];      // Q8_0 query codes (Q8_0 / Turbo4 caches)
-    __shared__ float qs_d[MAXG * 8];         // Q8_0 query block scales
-    __shared__ float sc[MAXG][ATT_TILE];     // scores → probabilities of one tile
-    __shared__ float m_run[MAXG], l_run[MAXG], alpha[MAXG];
+    __shared__ float qs_f[MG * 256];   // query heads of the group (f32; rotated for Turbo4)
+    __shared__ __align__(16) int8_t qs_i[MG * 256];  // their Q8_0 codes (Q8_0 / Turbo4 caches)
+    __shared__ float qs_d[MG * 8];     // Q8_0 block scales
+    __shared__ float sc[MG][TP];       // scores → probabilities of one tile
+    __shared__ float m_run[MG], l_run[MG], alpha[MG];
 
     for (int i = tid; i < G * hd; i += 256) qs_f[i] = a.q[(size_t)t * qd + (size_t)g * G * hd + i];
-    if (tid < MAXG) {
+    if (tid < MG) {
         m_run[tid] = -INFINITY;
         l_run[tid] = 0.0f;
     }
     __syncthreads();
-    if (a.kv_type != 0) {
+    if constexpr (KVT != 0) {
         // the query is rotated (Turbo4) and quantized to Q8_0 once (cpu.rs:585-598)
-        if (a.kv_type == 2) {
-            // rotation: signs then FWHT per block, one head per loop iteration
-            const int b = turbo_block(hd);
+        if constexpr (KVT == 2) {
             for (int j = 0; j < G; j++) {
                 float *x = qs_f + j * hd;
                 for (int e = tid; e < hd; e += 256) x[e] *= a.turbo_signs[e];
                 __syncthreads();
-                for (int hstep = 1; hstep < b; hstep *= 2) {
+                for (int hstep = 1; hstep < tb; hstep *= 2) {
                     for (int k = tid; k < hd / 2; k += 256) {
-                        const int blk = k / (b / 2), kk = k % (b / 2);
-                        const int jj = blk * b + (kk / hstep) * 2 * hstep + (kk % hstep);
+                        const int blk = k / (tb / 2), kk = k % (tb / 2);
+                        const int jj = blk * tb + (kk / hstep) * 2 * hstep + (kk % hstep);
                         const float x0 = x[jj], x1 = x[jj + hstep];
                         x[jj] = x0 + x1;
                         x[jj + hstep] = x0 - x1;
                     }
                     __syncthreads();
                 }
-                const float s = 1.0f / sqrtf((float)b);
-                for (int e = tid; e < hd; e += 256) x[e] *= s;
+                const float sq = 1.0f / sqrtf((float)tb);
+                for (int e = tid; e < hd; e += 256) x[e] *= sq;
                 __syncthreads();
             }
         }
@@ -270,82 +341,68 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         }
         __syncthreads();
     }
-
-    // V accumulation: an item is (head j, 8-dim chunk c); NI items, P groups of
-    // positions; each thread owns one (item, group) and 8 accumulators.
-    const int NI = G * (hd / 8);
-    const int P = max(1, 256 / NI);
-    const int item = tid % NI, pg = tid / NI;
-    const bool v_active = tid < NI * P;
-    const int vj = item / (hd / 8), vc = item % (hd / 8);
-    float o8[8];
+    // this lane's 8 query dims of every head of the group
+    float qf[MG][8];
+    uint32_t qq[MG][2];
+    float qdd[MG];
 #pragma unroll
-    for (int i = 0; i < 8; i++) o8[i] = 0.0f;
+    for (int j = 0; j < MG; j++) {
+        const int jj = j < G ? j : 0;
+        if constexpr (KVT == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) qf[j][i] = qs_f[jj * hd + d0 + i];
+        } else {
+            qq[j][0] = *(const uint32_t *)(qs_i + jj * hd + d0);
+            qq[j][1] = *(const uint32_t *)(qs_i + jj * hd + d0 + 4);
+            qdd[j] = qs_d[(jj * hd) / 32 + d0 / 32];
+        }
+    }
+    float o[MG][8];
+#pragma unroll
+    for (int j = 0; j < MG; j++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[j][i] = 0.0f;
 
     const size_t kv_row0 = (size_t)g * a.slots;
-    const size_t q8rb = (size_t)(hd / 32) * 34;
-    const int tb = turbo_block(hd);
-    for (int tile = r0; tile < r1; tile += ATT_TILE) {
-        const int nt = min(ATT_TILE, r1 - tile);
-        // ---- scores, one lane per position ----
-        if (tid < nt) {
-            const int slot = (tile + tid) % a.slots;
-            const size_t row = kv_row0 + slot;
-            float sj[MAXG];
+    for (int tile = r0; tile < r1; tile += TP) {
+        // ---- K and V of the tile, all loads in flight together ----
+        KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
+        bool ok[ATT_NP];
 #pragma unroll
-            for (int j = 0; j < MAXG; j++) sj[j] = 0.0f;
-            if (a.kv_type == 0) {
-                const uint4 *kr = (const uint4 *)(a.k_cache + row * hd * 2);
-                for (int c = 0; c < hd / 8; c++) {
-                    const uint4 kv = kr[c];
-                    const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+        for (int n = 0; n < ATT_NP; n++) {
+            const int pos = tile + pi + PP * n;
+            ok[n] = pos < r1;
+            const size_t row = kv_row0 + (size_t)((ok[n] ? pos : r0) % a.slots);
+            load_chunk<KVT>(a.k_cache, a.k_scale, row, hd, d0, tb, kc[n]);
+            load_chunk<KVT>(a.v_cache, a.v_scale, row, hd, d0, tb, vc[n]);
+        }
+        // ---- scores: partial dot over 8 dims, summed over the SUB lanes ----
+#pragma unroll
+        for (int n = 0; n < ATT_NP; n++) {
+#pragma unroll
+            for (int j = 0; j < MG; j++) {
+                float part = 0.0f;
+                if constexpr (KVT == 0) {
                     float kf[8];
+                    chunk_values<0>(kc[n], d0, kf);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        kf[2 * i] = h2f(w4[i] & 0xffff);
-                        kf[2 * i + 1] = h2f(w4[i] >> 16);
+                    for (int i = 0; i < 8; i++) part = fmaf(kf[i], qf[j][i], part);
+                } else {
+                    uint32_t kw[2];
+                    if constexpr (KVT == 1) {
+                        kw[0] = kc[n].raw.x;
+                        kw[1] = kc[n].raw.y;
+                    } else {
+                        turbo_levels8(kc[n], (d0 % 32) >= 16, kw);
                     }
-                    for (int j = 0; j < G; j++) {
-                        const float *qq = qs_f + j * hd + c * 8;
-#pragma unroll
-                        for (int i = 0; i < 8; i++) sj[j] = fmaf(kf[i], qq[i], sj[j]);
-                    }
+                    // the block's integer dot is exact over its 4 lanes (cpu.rs: per-block int32 sums)
+                    const int isum = quad_sum_i(sdot4(kw[1], qq[j][1], sdot4(kw[0], qq[j][0], 0)));
+                    const float ks = KVT == 1 ? h2f(kc[n].sc) : h2f(kc[n].sc) * (1.0f / 46.0f);
+                    part = (cact && (c & 3) == 0) ? (KVT == 1 ? ks * qdd[j] : qdd[j] * ks) * (float)isum : 0.0f;
                 }
-            } else if (a.kv_type == 1) {
-                const uint8_t *kr = a.k_cache + row * q8rb;
-                for (int bi = 0; bi < hd / 32; bi++) {
-                    const uint8_t *blk = kr + bi * 34;
-                    const float dk = h2f(blk[0] | (blk[1] << 8));
-                    int8_t kq[32];
-#pragma unroll
-                    for (int i = 0; i < 32; i++) kq[i] = (int8_t)blk[2 + i];
-                    for (int j = 0; j < G; j++) {
-                        const int8_t *qq = qs_i + j * hd + bi * 32;
-                        int acc = 0;
-#pragma unroll
-                        for (int i = 0; i < 32; i++) acc += (int)kq[i] * qq[i];
-                        sj[j] = fmaf(dk * qs_d[(j * hd) / 32 + bi], (float)acc, sj[j]);
-                    }
-                }
-            } else {
-                const uint8_t *kr = a.k_cache + row * (size_t)(hd / 2);
-                for (int bi = 0; bi < hd / 32; bi++) {
-                    int8_t lv[32];
-                    turbo_levels32(kr + bi * 16, lv);
-                    const float ks = h2f(a.k_scale[row * (hd / tb) + (bi * 32) / tb]);
-                    for (int j = 0; j < G; j++) {
-                        const int8_t *qq = qs_i + j * hd + bi * 32;
-                        int acc = 0;
-#pragma unroll
-                        for (int i = 0; i < 32; i++) acc += (int)lv[i] * qq[i];
-                        sj[j] = fmaf(qs_d[(j * hd) / 32 + bi] * ks * (1.0f / 46.0f), (float)acc, sj[j]);
-                    }
-                }
-            }
-            for (int j = 0; j < G; j++) {
-                float v = sj[j];
-                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
-                sc[j][tid] = v;
+                if (!cact) part = 0.0f;
+                const float sum = group_sum<SUB>(part);
+                if (c == 0 && j < G) sc[j][pi + PP * n] = ok[n] ? softcap_f(sum, a.softcap) : -INFINITY;
             }
         }
         __syncthreads();
@@ -353,11 +410,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         const int wv = tid >> 6, lane = tid & 63;
         for (int j = wv; j < G; j += 4) {
             float mx = -INFINITY;
-            for (int i = lane; i < nt; i += 64) mx = fmaxf(mx, sc[j][i]);
+            for (int i = lane; i < TP; i += 64) mx = fmaxf(mx, sc[j][i]);
             mx = wave_max(mx, 64);
             const float m_new = fmaxf(m_run[j], mx);
             float sum = 0.0f;
-            for (int i = lane; i < nt; i += 64) {
+            for (int i = lane; i < TP; i += 64) {
                 const float pv = expf(sc[j][i] - m_new);
                 sc[j][i] = pv;
                 sum += pv;
@@ -371,56 +428,50 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        // ---- V accumulation: 16-byte V-row loads per (item, position) ----
-        if (v_active) {
-            const float al = alpha[vj];
+        // ---- V: o[j] = alpha[j]·o[j] + Σ_pos p[j][pos]·v[pos] over this lane's 8 dims ----
 #pragma unroll
-            for (int i = 0; i < 8; i++) o8[i] *= al;
-            for (int pi = pg; pi < nt; pi += P) {
-                const size_t row = kv_row0 + (tile + pi) % a.slots;
-                const float pw = sc[vj][pi];
-                float vv[8];
-                if (a.kv_type == 0) {
-                    const uint4 w4 = *(const uint4 *)(a.v_cache + (row * hd + vc * 8) * 2);
-                    const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+        for (int j = 0; j < MG; j++) {
+            const float al = j < G ? alpha[j] : 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        vv[2 * i] = h2f(ww[i] & 0xffff);
-                        vv[2 * i + 1] = h2f(ww[i] >> 16);
-                    }
-                } else if (a.kv_type == 1) {
-                    const uint8_t *blk = a.v_cache + row * q8rb + (vc * 8 / 32) * 34;
-                    const float dv = h2f(blk[0] | (blk[1] << 8));
+            for (int i = 0; i < 8; i++) o[j][i] *= al;
+        }
 #pragma unroll
-                    for (int i = 0; i < 8; i++) vv[i] = dv * (float)(int8_t)blk[2 + (vc * 8) % 32 + i];
-                } else {
-                    const int d0 = vc * 8;
-                    const uint8_t *cb = a.v_cache + row * (size_t)(hd / 2) + (d0 / 32) * 16 + (d0 % 16);
-                    const bool hi = (d0 % 32) >= 16;
-                    const float vs = h2f(a.v_scale[row * (hd / tb) + d0 / tb]) * (1.0f / 46.0f);
+        for (int n = 0; n < ATT_NP; n++) {
+            float vv[8];
+            chunk_values<KVT>(vc[n], d0, vv);
 #pragma unroll
-                    for (int i = 0; i < 8; i++) vv[i] = vs * (float)KV_LEVELS_I8[hi ? (cb[i] >> 4) : (cb[i] & 15)];
-                }
+            for (int j = 0; j < MG; j++) {
+                const float w = j < G ? sc[j][pi + PP * n] : 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; i++) o8[i] = fmaf(pw, vv[i], o8[i]);
+                for (int i = 0; i < 8; i++) o[j][i] = fmaf(w, vv[i], o[j][i]);
             }
         }
         __syncthreads();
     }
-    // ---- reduce the position groups, write this range's partial ----
-    float *red = &sc[0][0];  // reuse the score tile: P·NI·8 ≤ 8·256 floats
-    if (v_active && pg > 0)
+    // ---- sum the position slots: inside the wave, then over the 4 waves in LDS ----
 #pragma unroll
-        for (int i = 0; i < 8; i++) red[((pg - 1) * NI + item) * 8 + i] = o8[i];
+    for (int off = SUB; off < 64; off <<= 1)
+#pragma unroll
+        for (int j = 0; j < MG; j++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[j][i] += __shfl_xor(o[j][i], off, 64);
+    float *wsum = qs_f;  // MG·256 floats: reused, the query now lives in registers
+    const int wv = tid >> 6, lane = tid & 63;
     __syncthreads();
+    for (int w = 0; w < 4; w++) {
+        if (wv == w && lane < SUB && cact) {
+#pragma unroll
+            for (int j = 0; j < MG; j++)
+                if (j < G)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) wsum[j * hd + d0 + i] = (w == 0 ? 0.0f : wsum[j * hd + d0 + i]) + o[j][i];
+        }
+        __syncthreads();
+    }
     float *part = a.part + (((size_t)t * a.n_head + (size_t)g * G) * a.n_split) * (hd + 2);
-    if (v_active && pg == 0) {
-        for (int q = 1; q < P; q++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) o8[i] += red[((q - 1) * NI + item) * 8 + i];
-        float *dst = part + ((size_t)vj * a.n_split + s_idx) * (hd + 2) + vc * 8;
-#pragma unroll
-        for (int i = 0; i < 8; i++) dst[i] = o8[i];
+    for (int i = tid; i < G * hd; i += 256) {
+        const int j = i / hd, d = i % hd;
+        part[((size_t)j * a.n_split + s_idx) * (hd + 2) + d] = wsum[i];
     }
     if (tid < G) {
         float *pp = part + ((size_t)tid * a.n_split + s_idx) * (hd + 2);
@@ -434,7 +485,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const int hd = a.hd;
     __shared__ float o_s[256];
-    __shared__ float wts[64];
+    __shared__ float wts[ATT_MAX_SPLIT];
+    __shared__ float acc_s[256];
     __shared__ float s_L;
     const float *part = a.part + ((size_t)t * a.n_head + h) * a.n_split * (hd + 2);
     if (tid < 64) {
@@ -453,13 +505,25 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
     __syncthreads();
     const float invL = 1.0f / s_L;
-    for (int d = tid; d < hd; d += 256) {
-        float o = 0.0f;
-        for (int s = 0; s < a.n_split; s++) {
-            const float w = wts[s];
-            if (w != 0.0f) o = fmaf(part[(size_t)s * (hd + 2) + d], w, o);
-        }
-        o_s[d] = o * invL;
+    // nh thread groups of hd threads, group k takes splits k, k+nh, …
+    const int nh = hd <= 128 ? 256 / hd : 1;
+    const int grp = tid / hd, d = tid % hd;
+    float o = 0.0f;
+    if (grp < nh) {
+#pragma unroll 4
+        for (int s = grp; s < a.n_split; s += nh) o = fmaf(part[(size_t)s * (hd + 2) + d], wts[s], o);
+    }
+    if (grp == 1 && grp < nh) acc_s[d] = o;
+    __syncthreads();
+    for (int k = 2; k < nh; k++) {  // more than two groups (hd ≤ 64): add in order
+        if (grp == k) acc_s[d] += o;
+        __syncthreads();
+    }
+    if (grp == 0) o_s[d] = (nh > 1 ? o + acc_s[d] : o) * invL;
+    for (int dd = 256 + tid; dd < hd; dd += 256) {  // hd > 256 is rejected by the host; kept for clarity
+        float x = 0.0f;
+        for (int s = 0; s < a.n_split; s++) x = fmaf(part[(size_t)s * (hd + 2) + dd], wts[s], x);
+        o_s[dd] = x * invL;
     }
     __syncthreads();
     if (a.kv_type == 2) {  // o ← Rᵀ o: block FWHT, then signs (turbo.rs:114-117)
@@ -509,8 +573,39 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
 }
 
+template <int KVT, int SUB>
+static void launch_split_g(const AttnArgs &a, int G, dim3 grid, hipStream_t st) {
+    if (G <= 2) hipLaunchKernelGGL((attn_split_kernel<KVT, SUB, 2>), grid, dim3(256), 0, st, a);
+    else if (G <= 4) hipLaunchKernelGGL((attn_split_kernel<KVT, SUB, 4>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((attn_split_kernel<KVT, SUB, 8>), grid, dim3(256), 0, st, a);
+}
+
+template <int KVT>
+static void launch_split_kvt(const AttnArgs &a, dim3 grid, hipStream_t st) {
+    const int G = a.n_head / a.n_kv;
+    const int sub = a.hd <= 16 ? 2 : a.hd <= 32 ? 4 : a.hd <= 64 ? 8 : a.hd <= 128 ? 16 : 32;
+    switch (sub) {
+    case 2: launch_split_g<KVT, 2>(a, G, grid, st); break;
+    case 4: launch_split_g<KVT, 4>(a, G, grid, st); break;
+    case 8: launch_split_g<KVT, 8>(a, G, grid, st); break;
+    case 16: launch_split_g<KVT, 16>(a, G, grid, st); break;
+    default: launch_split_g<KVT, 32>(a, G, grid, st); break;
+    }
+}
+
+int attention_splits(int n_tok, int n_kv, int max_len) {
+    if (n_tok > 1) return std::max(1, std::min(32, 2048 / std::max(1, n_tok * n_kv)));
+    // decode: at least 32 ranges, and ranges of at most 256 positions
+    return std::min(ATT_MAX_SPLIT, std::max(32, (max_len + 255) / 256));
+}
+
 void launch_attention(const AttnArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(attn_split_kernel, dim3(a.n_split, a.n_kv, a.n_tok), dim3(256), 0, st, a);
+    const dim3 grid(a.n_split, a.n_kv, a.n_tok);
+    switch (a.kv_type) {
+    case 0: launch_split_kvt<0>(a, grid, st); break;
+    case 1: launch_split_kvt<1>(a, grid, st); break;
+    default: launch_split_kvt<2>(a, grid, st); break;
+    }
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_head, a.n_tok), dim3(256), 0, st, a);
 }
 

@@ -73,7 +73,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
         const uint32_t *wp = (const uint32_t *)(row + 36 * u);
         uint32_t w[9];
 #pragma unroll
-        for (int i = 0; i < 9; i++) w[i] = __builtin_nontemporal_load(wp + i);
+        for (int i = 0; i < 9; i++) w[i] = wload(wp + i);
         const float d0 = h2f(w[0] & 0xffff), d1 = h2f(w[4] >> 16);
         uint32_t q[8];
 #pragma unroll
@@ -106,7 +106,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
         const uint32_t *wp = (const uint32_t *)(row + 68 * u);
         uint32_t w[17];
 #pragma unroll
-        for (int i = 0; i < 17; i++) w[i] = __builtin_nontemporal_load(wp + i);
+        for (int i = 0; i < 17; i++) w[i] = wload(wp + i);
         const float d0 = h2f(w[0] & 0xffff), d1 = h2f(w[8] >> 16);
         uint32_t q[8];
 #pragma unroll
@@ -129,9 +129,9 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
     } else if constexpr (TY == T_Q4_K) {
         const int sb = u >> 2, qi = u & 3;
         const uint8_t *b = row + 144 * sb;
-        const u32x4 hdr = ld_nt16(b);
-        const u32x4 v0 = ld_nt16(b + 16 + 32 * qi);
-        const u32x4 v1 = ld_nt16(b + 32 + 32 * qi);
+        const u32x4 hdr = ld_w16(b);
+        const u32x4 v0 = ld_w16(b + 16 + 32 * qi);
+        const u32x4 v1 = ld_w16(b + 32 + 32 * qi);
         const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
         int sc[2], mn[2];
         q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi, sc[0], mn[0]);
@@ -183,7 +183,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
             acc[tt] = fmaf(d * act.d[(size_t)t * nsb + sb], (float)sumi, acc[tt]);
         }
     } else if constexpr (TY == T_F32) {
-        const f32x4 w0 = ld_nt16f(row + 32 * u), w1 = ld_nt16f(row + 32 * u + 16);
+        const f32x4 w0 = ld_w16f(row + 32 * u), w1 = ld_w16f(row + 32 * u + 16);
 #pragma unroll
         for (int tt = 0; tt < MAXT; tt++) {
             if (tt >= nt) break;
@@ -195,7 +195,7 @@ __device__ __forceinline__ void unit_dot(const uint8_t *__restrict__ row, int u,
             acc[tt] = s;
         }
     } else if constexpr (TY == T_F16) {
-        const u32x4 wv = ld_nt16(row + 16 * u);
+        const u32x4 wv = ld_w16(row + 16 * u);
         const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
         for (int tt = 0; tt < MAXT; tt++) {
@@ -285,7 +285,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvP p) {
 struct DecP {
     SegP seg[3];
     int nseg, total_rows, K;
-    int tr;          // rows per workgroup
+    int tr;          // rows per workgroup; a workgroup never spans two segments
+    int blk_end[3];  // cumulative workgroup count at the end of each segment
     ActQ8 act;
     const float *actf;
     int glu;         // 0 none, 1 silu, 2 gelu
@@ -344,18 +345,62 @@ __device__ __forceinline__ void load_act(ActSlice<TY> &a, int u, const ActQ8 &ac
     }
 }
 
+// Raw bytes of one unit, loaded unconditionally so that the loads of all rows
+// of a pass are in flight together; dot_raw does the arithmetic afterwards.
+template <int TY> struct Raw;
+template <> struct Raw<T_Q4_0> { uint32_t w[9]; };
+template <> struct Raw<T_Q8_0> { uint32_t w[17]; };
+template <> struct Raw<T_Q4_K> { u32x4 hdr, v0, v1; };
+template <> struct Raw<T_Q6_K> { uint32_t ql[9], qh[9], sh_l, sh_h, scw, d; };
+template <> struct Raw<T_F32> { f32x4 a, b; };
+template <> struct Raw<T_F16> { u32x4 a; };
+
 template <int TY>
-__device__ __forceinline__ float dec_unit(const uint8_t *__restrict__ row, int u, const ActSlice<TY> &a) {
+__device__ __forceinline__ void load_raw(const uint8_t *__restrict__ row, int u, Raw<TY> &r) {
     if constexpr (TY == T_Q4_0) {
         const uint32_t *wp = (const uint32_t *)(row + 36 * u);
-        uint32_t w[9];
 #pragma unroll
-        for (int i = 0; i < 9; i++) w[i] = __builtin_nontemporal_load(wp + i);
+        for (int i = 0; i < 9; i++) r.w[i] = wload(wp + i);
+    } else if constexpr (TY == T_Q8_0) {
+        const uint32_t *wp = (const uint32_t *)(row + 68 * u);
+#pragma unroll
+        for (int i = 0; i < 17; i++) r.w[i] = wload(wp + i);
+    } else if constexpr (TY == T_Q4_K) {
+        const int sb = u >> 2, qi = u & 3;
+        const uint8_t *b = row + 144 * sb;
+        r.hdr = wload((const u32x4 *)b);
+        r.v0 = wload((const u32x4 *)(b + 16 + 32 * qi));
+        r.v1 = wload((const u32x4 *)(b + 32 + 32 * qi));
+    } else if constexpr (TY == T_Q6_K) {
+        const int sb = u >> 3, rr = u & 7, n = rr >> 2, k = rr & 3;
+        const uint8_t *b = row + 210 * sb;
+        const uintptr_t al = (uintptr_t)(b + 64 * n + 32 * (k & 1)), ah = (uintptr_t)(b + 128 + 32 * n);
+        const uint32_t *ql = (const uint32_t *)(al & ~(uintptr_t)3), *qh = (const uint32_t *)(ah & ~(uintptr_t)3);
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            r.ql[i] = wload(ql + i);
+            r.qh[i] = wload(qh + i);
+        }
+        r.sh_l = (uint32_t)(al & 3);
+        r.sh_h = (uint32_t)(ah & 3);
+        r.scw = wload((const uint16_t *)(b + 192 + 8 * n + 2 * k));
+        r.d = wload((const uint16_t *)(b + 208));
+    } else if constexpr (TY == T_F32) {
+        r.a = wload((const f32x4 *)(row + 32 * u));
+        r.b = wload((const f32x4 *)(row + 32 * u + 16));
+    } else {
+        r.a = wload((const u32x4 *)(row + 16 * u));
+    }
+}
+
+template <int TY>
+__device__ __forceinline__ float dot_raw(const Raw<TY> &r, int u, const ActSlice<TY> &a) {
+    if constexpr (TY == T_Q4_0) {
         uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++) q[4 + i] = w[5 + i];
+        for (int i = 0; i < 4; i++) q[4 + i] = r.w[5 + i];
         int i0 = 0, i1 = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -366,30 +411,22 @@ __device__ __forceinline__ float dec_unit(const uint8_t *__restrict__ row, int u
         }
         i0 -= 8 * a.i0;
         i1 -= 8 * a.i1;
-        const float r0 = h2f(w[0] & 0xffff) * a.d0 * (float)i0;
-        return fmaf(h2f(w[4] >> 16) * a.d1, (float)i1, r0);
+        const float r0 = h2f(r.w[0] & 0xffff) * a.d0 * (float)i0;
+        return fmaf(h2f(r.w[4] >> 16) * a.d1, (float)i1, r0);
     } else if constexpr (TY == T_Q8_0) {
-        const uint32_t *wp = (const uint32_t *)(row + 68 * u);
-        uint32_t w[17];
-#pragma unroll
-        for (int i = 0; i < 17; i++) w[i] = __builtin_nontemporal_load(wp + i);
         int i0 = 0, i1 = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) i0 = sdot4(__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2), a.q[i], i0);
+        for (int i = 0; i < 8; i++) i0 = sdot4(__builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2), a.q[i], i0);
 #pragma unroll
-        for (int i = 0; i < 8; i++) i1 = sdot4(w[9 + i], a.q[8 + i], i1);
-        const float r0 = h2f(w[0] & 0xffff) * a.d0 * (float)i0;
-        return fmaf(h2f(w[8] >> 16) * a.d1, (float)i1, r0);
+        for (int i = 0; i < 8; i++) i1 = sdot4(r.w[9 + i], a.q[8 + i], i1);
+        const float r0 = h2f(r.w[0] & 0xffff) * a.d0 * (float)i0;
+        return fmaf(h2f(r.w[8] >> 16) * a.d1, (float)i1, r0);
     } else if constexpr (TY == T_Q4_K) {
-        const int sb = u >> 2, qi = u & 3;
-        const uint8_t *b = row + 144 * sb;
-        const u32x4 hdr = ld_nt16(b);
-        const u32x4 v0 = ld_nt16(b + 16 + 32 * qi);
-        const u32x4 v1 = ld_nt16(b + 32 + 32 * qi);
+        const int qi = u & 3;
         int sc[2], mn[2];
-        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi, sc[0], mn[0]);
-        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * qi + 1, sc[1], mn[1]);
-        const uint32_t v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * qi, sc[0], mn[0]);
+        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * qi + 1, sc[1], mn[1]);
+        const uint32_t v[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
         int s1 = 0, s2 = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -398,33 +435,28 @@ __device__ __forceinline__ float dec_unit(const uint8_t *__restrict__ row, int u
         }
         const int sumi = s1 * sc[0] + s2 * sc[1];
         const int summ = mn[0] * ((int)a.bs[0] + a.bs[1]) + mn[1] * ((int)a.bs[2] + a.bs[3]);
-        return (h2f(hdr.x & 0xffff) * a.d0) * (float)sumi - (h2f(hdr.x >> 16) * a.d0) * (float)summ;
+        return (h2f(r.hdr.x & 0xffff) * a.d0) * (float)sumi - (h2f(r.hdr.x >> 16) * a.d0) * (float)summ;
     } else if constexpr (TY == T_Q6_K) {
-        const int sb = u >> 3, r = u & 7, n = r >> 2, k = r & 3;
-        const uint8_t *b = row + 210 * sb;
-        uint32_t ql[8], qh[8];
-        load32_a2(b + 64 * n + 32 * (k & 1), ql);
-        load32_a2(b + 128 + 32 * n, qh);
-        const uint16_t scw = *(const uint16_t *)(b + 192 + 8 * n + 2 * k);
+        const int k = u & 3;
         const int sh = k >= 2 ? 4 : 0, hs = 2 * k;
         int dl = 0, dh = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t v = ((ql[j] >> sh) & M4) | (((qh[j] >> hs) & 0x03030303u) << 4);
+            const uint32_t ql = __builtin_amdgcn_alignbyte(r.ql[j + 1], r.ql[j], r.sh_l);
+            const uint32_t qh = __builtin_amdgcn_alignbyte(r.qh[j + 1], r.qh[j], r.sh_h);
+            const uint32_t v = ((ql >> sh) & M4) | (((qh >> hs) & 0x03030303u) << 4);
             if (j < 4) dl = sdot4(v, a.q[j], dl);
             else dh = sdot4(v, a.q[j], dh);
         }
-        const int sumi = (int)(int8_t)(scw & 0xff) * (dl - 32 * a.bs[0]) + (int)(int8_t)(scw >> 8) * (dh - 32 * a.bs[1]);
-        return h2f(*(const uint16_t *)(b + 208)) * a.d0 * (float)sumi;
+        const int sumi = (int)(int8_t)(r.scw & 0xff) * (dl - 32 * a.bs[0]) + (int)(int8_t)(r.scw >> 8) * (dh - 32 * a.bs[1]);
+        return h2f(r.d) * a.d0 * (float)sumi;
     } else if constexpr (TY == T_F32) {
-        const f32x4 w0 = ld_nt16f(row + 32 * u), w1 = ld_nt16f(row + 32 * u + 16);
         float s = 0.0f;
-        s = fmaf(w0.x, a.f[0], s); s = fmaf(w0.y, a.f[1], s); s = fmaf(w0.z, a.f[2], s); s = fmaf(w0.w, a.f[3], s);
-        s = fmaf(w1.x, a.f[4], s); s = fmaf(w1.y, a.f[5], s); s = fmaf(w1.z, a.f[6], s); s = fmaf(w1.w, a.f[7], s);
+        s = fmaf(r.a.x, a.f[0], s); s = fmaf(r.a.y, a.f[1], s); s = fmaf(r.a.z, a.f[2], s); s = fmaf(r.a.w, a.f[3], s);
+        s = fmaf(r.b.x, a.f[4], s); s = fmaf(r.b.y, a.f[5], s); s = fmaf(r.b.z, a.f[6], s); s = fmaf(r.b.w, a.f[7], s);
         return s;
     } else {
-        const u32x4 wv = ld_nt16(row + 16 * u);
-        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        const uint32_t wd[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -435,82 +467,82 @@ __device__ __forceinline__ float dec_unit(const uint8_t *__restrict__ row, int u
     }
 }
 
+// rows whose loads a wave keeps in flight together (register budget ≈ R × unit bytes)
+#ifndef RIE_DEC_ROWS_SMALL
+#define RIE_DEC_ROWS_SMALL 4  // units of ≤ 48 bytes: Q4_0, Q4_K, F16
+#endif
+#ifndef RIE_DEC_ROWS_LARGE
+#define RIE_DEC_ROWS_LARGE 2  // Q8_0, Q6_K, F32
+#endif
 template <int TY>
-constexpr int dec_rows_per_pass() { return (TY == T_Q8_0 || TY == T_Q6_K || TY == T_F32) ? 2 : 4; }
-
-// Row pointer of (clamped) row r: the segments are stacked in row order
-// (GLU: gate rows only; the matching up row has the same index in seg[1]).
-__device__ __forceinline__ const uint8_t *dec_row(const DecP &p, int r) {
-    int rr = r;
-    const uint8_t *w = p.seg[0].w;
-    size_t rb = p.seg[0].rb;
-    if (!p.glu && p.nseg > 1 && rr >= p.seg[0].rows) {
-        rr -= p.seg[0].rows;
-        if (p.nseg > 2 && rr >= p.seg[1].rows) {
-            rr -= p.seg[1].rows;
-            w = p.seg[2].w;
-            rb = p.seg[2].rb;
-        } else {
-            w = p.seg[1].w;
-            rb = p.seg[1].rb;
-        }
-    }
-    return w + (size_t)rr * rb;
-}
+constexpr int dec_rows_per_pass() { return (TY == T_Q8_0 || TY == T_Q6_K || TY == T_F32) ? RIE_DEC_ROWS_LARGE : RIE_DEC_ROWS_SMALL; }
 
 constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 
-template <int TY, int LPR, int UPL>
+template <int TY, int LPR, int UPL, bool GLU>
 __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     constexpr int GROUPS = 256 / LPR;
     constexpr int R = dec_rows_per_pass<TY>();
     constexpr int STRIDE = LPR + DEC_PAD;
-    extern __shared__ float red[];  // [glu ? 2 : 1][tr][STRIDE], then tr floats of h
+    constexpr int NW = GLU ? 2 : 1;
+    extern __shared__ float red[];  // [NW][tr][STRIDE], then tr floats of h
     const int tid = threadIdx.x;
-    const int grp = tid / LPR, l = tid % LPR;
+    const int grp = LPR >= 64 ? __builtin_amdgcn_readfirstlane(tid / LPR) : tid / LPR;
+    const int l = tid % LPR;
     const int U = units_per_row<TY>(p.K);
     ActSlice<TY> a[UPL];
+    bool valid[UPL];
+    int uu[UPL];
 #pragma unroll
-    for (int k = 0; k < UPL; k++)
-        if (l + LPR * k < U) load_act<TY>(a[k], l + LPR * k, p.act, p.actf, p.K);
-    const int row0 = blockIdx.x * p.tr;
-    const int last = p.total_rows - 1;
-    // R rows per pass: the loads of all R rows are issued before their dots
+    for (int k = 0; k < UPL; k++) {
+        valid[k] = l + LPR * k < U;
+        uu[k] = valid[k] ? l + LPR * k : U - 1;  // idle lanes load a real unit and drop it
+        if (valid[k]) load_act<TY>(a[k], uu[k], p.act, p.actf, p.K);
+    }
+    // workgroup → (segment, first row): uniform, so the segment's fields are scalar
+    const int bid = blockIdx.x;
+    const int sg = (!GLU && p.nseg > 1 && bid >= p.blk_end[0]) ? ((p.nseg > 2 && bid >= p.blk_end[1]) ? 2 : 1) : 0;
+    const int row0 = (bid - (sg ? p.blk_end[sg - 1] : 0)) * p.tr;
+    const int seg_rows = p.seg[sg].rows;
+    const int last = seg_rows - 1;
+    const uint8_t *wbase = p.seg[sg].w;
+    const size_t rb = p.seg[sg].rb;
     for (int base = grp * R; base < p.tr; base += GROUPS * R) {
-        float acc[R], acc2[R];
+        Raw<TY> raw[NW][R][UPL];
 #pragma unroll
         for (int k = 0; k < R; k++) {
             const int r = min(row0 + base + k, last);
-            const uint8_t *row = dec_row(p, r);
-            float s = 0.0f;
+            const uint8_t *row = wbase + (size_t)r * rb;
 #pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (l + LPR * u < U) s += dec_unit<TY>(row, l + LPR * u, a[u]);
-            acc[k] = s;
-            if (p.glu) {
+            for (int u = 0; u < UPL; u++) load_raw<TY>(row, uu[u], raw[0][k][u]);
+            if constexpr (GLU) {
                 const uint8_t *row2 = p.seg[1].w + (size_t)r * p.seg[1].rb;
-                float s2 = 0.0f;
 #pragma unroll
-                for (int u = 0; u < UPL; u++)
-                    if (l + LPR * u < U) s2 += dec_unit<TY>(row2, l + LPR * u, a[u]);
-                acc2[k] = s2;
+                for (int u = 0; u < UPL; u++) load_raw<TY>(row2, uu[u], raw[1][k][u]);
             }
         }
 #pragma unroll
-        for (int k = 0; k < R; k++) {
-            red[(base + k) * STRIDE + l] = acc[k];
-            if (p.glu) red[(p.tr + base + k) * STRIDE + l] = acc2[k];
-        }
+        for (int wv = 0; wv < NW; wv++)
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                float s = 0.0f;
+#pragma unroll
+                for (int u = 0; u < UPL; u++) {
+                    const float x = dot_raw<TY>(raw[wv][k][u], uu[u], a[u]);
+                    s += valid[u] ? x : 0.0f;
+                }
+                red[(wv * p.tr + base + k) * STRIDE + l] = s;
+            }
     }
     __syncthreads();
     // 8 threads per row add its LPR partials
-    float *hv = red + (p.glu ? 2 : 1) * p.tr * STRIDE;
+    float *hv = red + NW * p.tr * STRIDE;
     const int s8 = tid & 7;
     for (int i = tid >> 3; i < ((p.tr + 31) & ~31); i += 32) {
         float sum = 0.0f, sum2 = 0.0f;
         if (i < p.tr) {
             for (int j = s8; j < LPR; j += 8) sum += red[i * STRIDE + j];
-            if (p.glu)
+            if constexpr (GLU)
                 for (int j = s8; j < LPR; j += 8) sum2 += red[(p.tr + i) * STRIDE + j];
         }
 #pragma unroll
@@ -519,34 +551,21 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
             sum2 += __shfl_xor(sum2, o, 64);
         }
         const int r = row0 + i;
-        if (s8 == 0 && i < p.tr && r < p.total_rows) {
+        if (s8 == 0 && i < p.tr && r < seg_rows) {
             float v = sum;
-            if (p.glu) v = (p.glu == 2 ? gelu_tanh_f(sum) : silu_f(sum)) * sum2;
-            int rr = r;
-            float *out = p.seg[0].out;
-            int epi = p.seg[0].epi;
-            if (!p.glu && p.nseg > 1 && rr >= p.seg[0].rows) {
-                rr -= p.seg[0].rows;
-                if (p.nseg > 2 && rr >= p.seg[1].rows) {
-                    rr -= p.seg[1].rows;
-                    out = p.seg[2].out;
-                    epi = p.seg[2].epi;
-                } else {
-                    out = p.seg[1].out;
-                    epi = p.seg[1].epi;
-                }
-            }
-            if (epi == EPI_ADD) out[rr] += v;
-            else out[rr] = v;
+            if constexpr (GLU) v = (p.glu == 2 ? gelu_tanh_f(sum) : silu_f(sum)) * sum2;
+            float *out = p.seg[sg].out;
+            if (p.seg[sg].epi == EPI_ADD) out[r] += v;
+            else out[r] = v;
             hv[i] = v;
         }
     }
-    if (!(p.glu && p.hq.qs)) return;
+    if (!(GLU && p.hq.qs)) return;
     // Q8_0 of h (ops: avx2 quantizer semantics), one half-wave per 32 rows
     __syncthreads();
     if (tid < p.tr) {
         const int r = row0 + tid;
-        const float y = r < p.total_rows ? hv[tid] : 0.0f;
+        const float y = r < seg_rows ? hv[tid] : 0.0f;
         float amax = fabsf(y);
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
@@ -560,7 +579,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
             su += __shfl_xor(su, o, 64);
             scl += __shfl_xor(scl, o, 64);
         }
-        if (r < p.total_rows) {
+        if (r < seg_rows) {
             p.hq.qs[r] = (int8_t)qc;
             if ((r & 31) == 0) {
                 p.hq.d[r >> 5] = d;
@@ -603,8 +622,17 @@ static bool launch_dec_t(DecP p, hipStream_t st) {
     p.tr = pass * m;
     const size_t lds = ((size_t)(p.glu ? 2 : 1) * p.tr * (lpr + DEC_PAD) + p.tr) * sizeof(float);
     if (lds > 64 * 1024) return false;
-    const int blocks = (p.total_rows + p.tr - 1) / p.tr;
-#define RIE_DEC(L, UP) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP>), dim3(blocks), dim3(256), lds, st, p)
+    int blocks = 0;
+    const int nseg = p.glu ? 1 : p.nseg;
+    for (int i = 0; i < 3; i++) {
+        if (i < nseg) blocks += (p.seg[i].rows + p.tr - 1) / p.tr;
+        p.blk_end[i] = blocks;
+    }
+#define RIE_DEC(L, UP)                                                                        \
+    do {                                                                                      \
+        if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true>), dim3(blocks), dim3(256), lds, st, p);  \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false>), dim3(blocks), dim3(256), lds, st, p);       \
+    } while (0)
     if (upl == 1) {
         switch (lpr) {
         case 16: RIE_DEC(16, 1); break;
@@ -688,7 +716,7 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
     int i = 0;
     while (i < nseg) {
         int j = i + 1;
-        while (j < nseg && segs[j].w.ty == segs[i].w.ty) j++;
+        while (j < nseg && j - i < 3 && segs[j].w.ty == segs[i].w.ty) j++;
         GemvP p{};
         p.nseg = j - i;
         p.total_rows = 0;
