@@ -39,13 +39,15 @@ def main():
     ap.add_argument("--gen", type=int, default=128)
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default: min(16, cores))")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true", help="short run of the roofline kernel (for counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the forward loop on one GPU; runs on more than one GPU are not part of this build",
               file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
+    if args.kernel_only:
+        return kernel_only(args)
     import torch
 
     import rust_interference_engine_amd as R
@@ -92,12 +94,13 @@ def main():
     pp_tps = args.prompt * args.steps / pp_t
 
     # ---- roofline of the dominant decode kernel, timed live with HIP events ----
+    # (the single-token gate/up/SwiGLU launch over every layer's weights in turn,
+    # on the backend's stream, so each launch streams its weights from HBM)
+    glu_us, glu_bytes = be.time_ffn_glu(reps=3)
+    glu_s = glu_us / 1e6
+    achieved = glu_bytes / glu_s / 1e9
     ctx_mid = args.prompt + args.gen // 2
     prof = be.profile_decode(ctx_mid, reps=5)
-    glu_ms, glu_n = prof["matmul_gate_up_glu"]
-    glu_bytes = 2 * q4_0_bytes(FF, E) + E + (E // 32) * 8 + FF * 4  # weights + Q8_0 activation + h
-    glu_s = glu_ms / glu_n / 1e3
-    achieved = glu_bytes / glu_s / 1e9
     step_ms = sum(v[0] for v in prof.values()) / 5
     layer_w = q4_0_bytes(qd, E) + 2 * q4_0_bytes(kvd, E) + q4_0_bytes(E, qd) + 3 * q4_0_bytes(FF, E)
     tok_bytes = L * layer_w + q4_0_bytes(V, E) + E // 32 * 18 + L * 2 * kvd * 2 * (ctx_mid + 1)
@@ -122,10 +125,11 @@ def main():
         "decode_bytes_per_token": tok_bytes,
         "decode_effective_gbs": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9, 1),
         "decode_frac_hbm_roofline": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "gemv gate+up+SwiGLU (Q4_0 x Q8_0)", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_s * 1e6, 2)},
-        "decode_kernel_ms": {k: round(v[0] / 5, 4) for k, v in prof.items()},
+        "roofline": {"bound": "hbm", "kernel": "gemv_dec_kernel gate+up+SwiGLU (Q4_0 x Q8_0, Q8_0 hidden out)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_us, 2)},
+        "eager_decode_kernel_ms": {k: round(v[0] / 5, 4) for k, v in prof.items()},
         "eager_decode_step_ms": round(step_ms, 3),
         "setup_s": {"synthesize": round(t_gen, 1), "upload": round(t_load, 1)},
         "greedy_head": [int(t) for t in toks[:8]],
@@ -133,6 +137,41 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(img, V, args)
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per gate/up/SwiGLU launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size)."""
+    path = os.path.join(ROOT, "profiles", "gemv_dec_gate_up_glu_llama8b_q4_0_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def kernel_only(args):
+    """Short run for counter collection: the gate/up/SwiGLU launch over all
+    layers, then a device copy of known size that calibrates the counters."""
+    import torch
+
+    import rust_interference_engine_amd as R
+    from rust_interference_engine_amd import synth
+
+    spec = synth.baseline_llama31_8b_q4_0(seed=1, ctx=8192)
+    img = synth.build_array(spec)
+    be = R.HipBackend(img, n_ctx=64, max_batch=8, kv_type=R.KvType.F16)
+    be.forward_argmax([13, 7932, 15851], 0)
+    us, nb = be.time_ffn_glu(reps=1)
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"ffn_glu_avg_us": round(us, 2), "bytes_per_launch": nb, "copy_bytes": n}), flush=True)
 
 
 def cpu_baseline(img, V, args):

@@ -141,6 +141,14 @@ size_t rie_hip_kv_row_bytes(const rie_hip_backend *b);
 int32_t rie_hip_profile_decode(rie_hip_backend *b, size_t pos, int32_t reps, char *names, size_t names_len, double *ms,
                                int32_t *launches, size_t max_entries, size_t *n_entries);
 
+/* Average duration in microseconds of the single-token gate/up/SwiGLU launch
+ * (dense_ffn's gate·x, up·x and silu product, model/cpu.rs:431-467, as one
+ * kernel), timed with HIP events on the backend's stream while cycling through
+ * every layer's weights reps times; *bytes_per_launch = weight bytes of gate
+ * and up + activation read + hidden written.  No counterpart in the reference:
+ * it measures the dominant decode kernel for the roofline report. */
+int32_t rie_hip_time_ffn_glu(rie_hip_backend *b, int32_t reps, double *avg_us, size_t *bytes_per_launch);
+
 /* ---- kernel entry points on device pointers (stream 0, synchronous) ---- */
 /* RMSNorm (w may be NULL: quantize only) + Q8_0 (fmt 1) or Q8_K (fmt 2) quantization
  * of n rows of k values (quant/mod.rs:191-218, kernels/avx2.rs:153-184).  Outputs:

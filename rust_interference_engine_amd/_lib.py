@@ -67,6 +67,7 @@ def lib():
         "rie_hip_capture": (I, [P, S, I, P, S]),
         "rie_hip_kv_layer": (I, [P, S, I, P, S, P, S]),
         "rie_hip_profile_decode": (I, [P, S, I, CP, S, P, P, S, C.POINTER(S)]),
+        "rie_hip_time_ffn_glu": (I, [P, I, C.POINTER(D), C.POINTER(S)]),
         "rie_hip_k_rmsnorm_quant": (I, [P, P, F, I, I, I, P, P, P, P, P, P]),
         "rie_hip_k_gemv": (I, [I, P, I, I, P, P, P, P, P, P, I, P]),
         "rie_hip_k_gemm": (I, [I, P, I, I, P, P, P, P, P, I, P]),

@@ -144,6 +144,14 @@ class HipBackend:
         keys = names.value.decode().split("\n")[: n.value]
         return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(keys)}
 
+    def time_ffn_glu(self, reps: int = 3) -> tuple[float, int]:
+        """(average µs, algorithmic bytes) of one single-token gate/up/SwiGLU launch"""
+        us, nb = C.c_double(), C.c_size_t()
+        rc = _lib.lib().rie_hip_time_ffn_glu(self._h, reps, C.byref(us), C.byref(nb))
+        if rc:
+            raise RieError(rc, "time_ffn_glu failed")
+        return us.value, nb.value
+
     # ---- parity hooks ----
     def set_capture(self, on: bool) -> None:
         _lib.lib().rie_hip_set_capture(self._h, int(on))

@@ -626,6 +626,51 @@ void HipBackend::mark(const char *name) {
     marks_.emplace_back(name, e);
 }
 
+double HipBackend::time_ffn_glu(int reps, size_t *bytes) {
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd;
+    if (reps < 1) throw rt_err("reps must be positive");
+    for (const auto &L : layers_)
+        if (L.moe) throw Error{E_UNSUPPORTED, "unsupported: gate/up timing of a MoE layer"};
+    RIE_HIP_CHECK(hipSetDevice(device_));
+    const DevLayer &L0 = layers_[0];
+    const DevWeight *ws[2] = {&L0.gate, &L0.up};
+    prepare(d_x_, L0.ffn_norm, 1, E, ws, 2, false);
+    const int fmt_in = act_format(L0.gate.ty);
+    const ActQ8 &a = fmt_in == ACT_Q8K ? actk_ : act0_;
+    auto one_pass = [&](size_t *b) {
+        for (const auto &L : layers_) {
+            const int ff = (int)L.ff;
+            const bool hq = act_format(L.down.ty) == ACT_Q8_0 && ff % 32 == 0;
+            bool done = hq && launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, &act_h_, st_);
+            if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, nullptr, st_))
+                throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
+            if (b && !*b) {  // weights + activation read + hidden (and its Q8_0) written
+                size_t in = fmt_in == ACT_F32 ? (size_t)E * 4
+                                              : fmt_in == ACT_Q8_0 ? (size_t)E + (size_t)E / 32 * (L.gate.ty == T_Q4_0 ? 8 : 4)
+                                                                   : (size_t)E + (size_t)E / 256 * 4 + (size_t)E / 16 * 2;
+                *b = L.gate.rows * L.gate.rb() + L.up.rows * L.up.rb() + in + (size_t)ff * 4 + (done ? (size_t)ff + (size_t)ff / 32 * 12 : 0);
+            }
+        }
+    };
+    size_t b = 0;
+    one_pass(&b);  // warm-up
+    check_launch("ffn glu timing");
+    hipEvent_t e0, e1;
+    RIE_HIP_CHECK(hipEventCreate(&e0));
+    RIE_HIP_CHECK(hipEventCreate(&e1));
+    RIE_HIP_CHECK(hipEventRecord(e0, st_));
+    for (int r = 0; r < reps; r++) one_pass(nullptr);
+    RIE_HIP_CHECK(hipEventRecord(e1, st_));
+    RIE_HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0;
+    RIE_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *bytes = b;
+    return (double)ms * 1e3 / ((double)reps * layers_.size());
+}
+
 // One eager decode step per repetition at position pos, with an event after
 // every launch on the backend's stream; returns per-kernel-family totals.
 std::vector<HipBackend::KernelTime> HipBackend::profile_decode(size_t pos, int reps) {

@@ -68,6 +68,9 @@ class HipBackend {
         int launches = 0;
     };
     std::vector<KernelTime> profile_decode(size_t pos, int reps);
+    // Average duration (µs) of the single-token gate/up/SwiGLU launch, cycling
+    // through every layer's weights; *bytes = algorithmic bytes of one launch.
+    double time_ffn_glu(int reps, size_t *bytes);
 
   private:
     struct DevLayer {

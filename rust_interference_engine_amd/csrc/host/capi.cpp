@@ -211,6 +211,10 @@ int32_t rie_hip_profile_decode(rie_hip_backend *b, size_t pos, int32_t reps, cha
     });
 }
 
+int32_t rie_hip_time_ffn_glu(rie_hip_backend *b, int32_t reps, double *avg_us, size_t *bytes_per_launch) {
+    return guarded(nullptr, 0, [&] { *avg_us = b->b->time_ffn_glu(reps, bytes_per_launch); });
+}
+
 // ---- kernel entry points ----
 int32_t rie_hip_k_rmsnorm_quant(const float *x, const float *w, float eps, int32_t n, int32_t k, int32_t fmt, float *xn, int8_t *qs,
                                 float *d, float *s, int32_t *isum, int16_t *bsums) {
