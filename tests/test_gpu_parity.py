@@ -148,6 +148,52 @@ def test_gemv_matches_oracle_rows(oracle, cuda, ty):
 
 
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
+def test_gemm_matches_oracle_rows(oracle, cuda, ty):
+    """The int8-MFMA prompt GEMM against the oracle's block dots, for row and
+    token counts that are not multiples of the 32×32 tiles."""
+    import ggml_np as G
+    r = oracle.Rng(31 + ty)
+    for k, rows, n_tok in ((64, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130)):
+        w = r.random_weight(ty, rows, k)
+        x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
+        act = _quant_on_gpu(x, 1, cuda)["dev"]
+        got = _gemv(ty, w, rows, k, act, None, n_tok, cuda, gemm=True)
+        wf = G.dequantize(ty, w, rows * k).reshape(rows, k).astype(np.float64)
+        rb = G.row_bytes(ty, k)
+        for t in range(n_tok):
+            a = oracle.quantize_act(ty, x[t])
+            want = np.array([oracle.vec_dot(ty, w[i * rb:(i + 1) * rb], a, k) for i in range(rows)])
+            mag = np.abs(wf * x[t].astype(np.float64)).sum(axis=1)
+            assert np.all(np.abs(got[t] - want) <= 1e-5 * mag + 1e-6), (ty, k, rows, n_tok, t)
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
+def test_gemm_per_block_integer_dots_exact(oracle, cuda, ty):
+    """One non-zero activation block per token: every GEMM output is one rounding
+    of (d_w·d_a)·idot, the reference's per-block term, for 40 tokens at once."""
+    r = oracle.Rng(6)
+    k, rows, n_tok = 1024, 64, 40
+    w = r.random_weight(ty, rows, k)
+    rng = np.random.default_rng(8)
+    x = np.zeros((n_tok, k), np.float32)
+    blocks = rng.integers(0, k // 32, n_tok)
+    for t in range(n_tok):
+        x[t, blocks[t] * 32:(blocks[t] + 1) * 32] = rng.standard_normal(32) * 3
+    act = _quant_on_gpu(x, 1, cuda)
+    got = _gemv(ty, w, rows, k, act["dev"], None, n_tok, cuda, gemm=True)
+    rb = (18 if ty == Q4_0 else 34) * k // 32
+    for t in range(n_tok):
+        b = blocks[t]
+        a = oracle.quantize_q8_0(x[t])
+        for i in range(rows):
+            idots = oracle.block_idots(ty, w[i * rb:(i + 1) * rb], a, k)
+            blk = w[i * rb + b * (rb * 32 // k): i * rb + b * (rb * 32 // k) + 2]
+            dw = np.frombuffer(blk.tobytes(), np.float16)[0].astype(np.float32)
+            want = np.float32(np.float32(dw * a["d"][b]) * np.float32(idots[b]))
+            assert got[t, i] == want, (t, b, i)
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
 def test_gemv_per_block_integer_dots_exact(oracle, cuda, ty):
     """With one non-zero activation block the row result is one rounding of
     (d_w·d_a)·idot, so it pins every per-block int32 dot exactly."""
@@ -221,6 +267,22 @@ def test_model_logits_match_oracle(oracle, cuda, arch, ty, kv, tol):
     for t, tok in enumerate(toks):  # token-by-token decode (graph replay)
         err = max_rel_err(g.forward([tok], t), o.forward([tok], t))
         assert err < tol, f"{arch} {ty} kv{kv}: decode token {t}: {err}"
+
+
+@pytest.mark.parametrize("arch,ty", [("llama", Q4_0), ("llama", Q8_0), ("qwen3", Q4_0), ("gemma2", Q8_0)])
+def test_prompt_batches_through_gemm_match_oracle(oracle, cuda, arch, ty):
+    """Prompt batches of 24 and 40 tokens run the int8-MFMA GEMM (fused Q/K/V,
+    wo, gate/up with SwiGLU/GELU, down) and must match the oracle like decode."""
+    from naive_model import max_rel_err
+    spec, g, o = _pair(oracle, arch, ty, 0, n_ctx=96, max_batch=40)
+    nv = spec.n_vocab
+    toks = [(i * 29 + 3) % nv for i in range(64)]
+    for pos, end in ((0, 24), (24, 64)):
+        lg = g.forward(toks[pos:end], pos, True)
+        lo = o.forward(toks[pos:end], pos, True)
+        for t in range(end - pos):
+            err = max_rel_err(lg[t * nv:(t + 1) * nv], lo[t * nv:(t + 1) * nv])
+            assert err < 0.03, f"{arch} {ty}: token {pos + t}: {err}"
 
 
 ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32, query groups 1..8
