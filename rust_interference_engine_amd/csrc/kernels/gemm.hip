@@ -28,8 +28,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int GEMM_WAVES = 4;                  // row tiles per workgroup
-constexpr int GEMM_ROWS = 32 * GEMM_WAVES;     // rows per workgroup
 
 struct GemmP {
     const uint8_t *w[3];
@@ -39,7 +37,7 @@ struct GemmP {
     int ld[3];
     int epi[3];
     int nseg;
-    int rg_end[3];  // cumulative row groups (GEMM_ROWS rows) at the end of each segment
+    int rg_end[3];  // cumulative row groups (64 rows) at the end of each segment
     int n_rg;       // row groups in total
     int n_tg;       // token groups
     int glu;        // 0 none; 1 silu / 2 gelu-tanh: seg 0 gate, seg 1 up, out[0] = h
@@ -61,72 +59,124 @@ __device__ __forceinline__ void load_wunit(const uint8_t *row, int b, WUnit<TY> 
     for (int i = 0; i < (TY == T_Q4_0 ? 9 : 17); i++) u.w[i] = wload(p + i);
 }
 
-// B operand (16 signed values of this lane's half) and d of block (b + j)
+// ---- LDS-tiled kernel ---------------------------------------------------------
+// Workgroup tile: 64 weight rows × 128 tokens, 4 waves as 2 (rows) × 2 (tokens),
+// each wave 32 rows × 64 tokens.  Per stage of KC = 4 blocks (128 values of K)
+// the workgroup stages the activation codes and scales and the weight codes
+// (nibbles kept packed, 16 B/block for Q4_0) and scales in LDS; the next
+// stage's global loads are in flight while the current stage is multiplied.
+constexpr int G_BM = 64, G_BN = 128, G_KC = 4;
+constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, padded)
+
 template <int TY>
-__device__ __forceinline__ v4i unpack_w(const WUnit<TY> &u, int j, int h, float &dw) {
-    v4i r;
-    if constexpr (TY == T_Q4_0) {
-        uint32_t q[4];
-        if (j == 0) {
-            dw = h2f(u.w[0] & 0xffff);
+struct GemmLds {
+    static constexpr int QB = TY == T_Q4_0 ? 16 : 32;  // weight code bytes per block in LDS
+    static constexpr int WST = G_KC * QB + 16;          // weight row stride (bytes, padded)
+};
+
+template <int TY, bool GLU>
+struct __align__(16) GemmStage {
+    static constexpr int NW = GLU ? 2 : 1;
+    int8_t a[G_BN * G_AST];
+    float da[G_BN * G_KC];
+    uint8_t wq[NW][G_BM * GemmLds<TY>::WST];
+    float dw[NW][G_BM * G_KC];
+};
+
+// registers holding one stage's global loads before they are written to LDS
+template <int TY, bool GLU>
+struct StageRegs {
+    static constexpr int NW = GLU ? 2 : 1;
+    v4i a[4];
+    float4 da;
+    WUnit<TY> w;
+};
+
+template <int TY, bool GLU>
+__device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int t0, int b0, int tid, StageRegs<TY, GLU> &R) {
+    const int K = p.K, nb = K >> 5;
+    {   // activation codes: thread → (token, 64-byte half of the 128-byte chunk)
+        const int tok = min(t0 + (tid >> 1), p.n_tok - 1);
+        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 32 * b0 + 64 * (tid & 1));
 #pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(u.w[i + 1], u.w[i], 2);
-        } else {
-            dw = h2f(u.w[4] >> 16);
-#pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = u.w[5 + i];
-        }
-        const uint32_t sh = 4u * (uint32_t)h;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t nib = (q[i] >> sh) & 0x0F0F0F0Fu;
-            r[i] = (int)((nib + 0x78787878u) ^ 0x80808080u);  // bytewise q − 8
-        }
-    } else {
-        if (j == 0) {
-            dw = h2f(u.w[0] & 0xffff);
-#pragma unroll
-            for (int i = 0; i < 4; i++) r[i] = (int)__builtin_amdgcn_alignbyte(u.w[4 * h + i + 1], u.w[4 * h + i], 2);
-        } else {
-            dw = h2f(u.w[8] >> 16);
-#pragma unroll
-            for (int i = 0; i < 4; i++) r[i] = (int)u.w[9 + 4 * h + i];
+        for (int i = 0; i < 4; i++) R.a[i] = src[i];
+    }
+    if (tid < G_BN) {
+        const int tok = min(t0 + tid, p.n_tok - 1);
+        R.da = *(const float4 *)(p.d + (size_t)tok * nb + b0);
+    }
+    {   // weights: thread → (matrix, row, 2-block unit)
+        const int nw = GLU ? (tid >> 7) : 0;
+        const int idx = tid & 127;
+        const int row = min(row0 + (idx >> 1), p.rows[GLU ? 0 : sg] - 1);
+        if (GLU || tid < 128) {
+            const int s = GLU ? nw : sg;
+            load_wunit<TY>(p.w[s] + (size_t)row * p.rb[s], b0 + 2 * (idx & 1), R.w);
         }
     }
-    return r;
 }
 
-template <int TY, int NT, bool GLU>
+template <int TY, bool GLU>
+__device__ __forceinline__ void stage_store(GemmStage<TY, GLU> &S, int tid, const StageRegs<TY, GLU> &R) {
+    {
+        v4i *dst = (v4i *)(S.a + (tid >> 1) * G_AST + 64 * (tid & 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = R.a[i];
+    }
+    if (tid < G_BN) *(float4 *)(S.da + tid * G_KC) = R.da;
+    if (GLU || tid < 128) {
+        const int nw = GLU ? (tid >> 7) : 0;
+        const int idx = tid & 127, row = idx >> 1, u = idx & 1;
+        constexpr int QB = GemmLds<TY>::QB, WST = GemmLds<TY>::WST;
+        uint8_t *wq = S.wq[nw] + row * WST + 2 * u * QB;
+        float *dw = S.dw[nw] + row * G_KC + 2 * u;
+        if constexpr (TY == T_Q4_0) {
+            uint4 q0, q1;
+            q0.x = __builtin_amdgcn_alignbyte(R.w.w[1], R.w.w[0], 2);
+            q0.y = __builtin_amdgcn_alignbyte(R.w.w[2], R.w.w[1], 2);
+            q0.z = __builtin_amdgcn_alignbyte(R.w.w[3], R.w.w[2], 2);
+            q0.w = __builtin_amdgcn_alignbyte(R.w.w[4], R.w.w[3], 2);
+            q1 = make_uint4(R.w.w[5], R.w.w[6], R.w.w[7], R.w.w[8]);
+            *(uint4 *)wq = q0;
+            *(uint4 *)(wq + 16) = q1;
+            dw[0] = h2f(R.w.w[0] & 0xffff);
+            dw[1] = h2f(R.w.w[4] >> 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) ((uint32_t *)wq)[i] = __builtin_amdgcn_alignbyte(R.w.w[i + 1], R.w.w[i], 2);
+#pragma unroll
+            for (int i = 0; i < 8; i++) ((uint32_t *)wq)[8 + i] = R.w.w[9 + i];
+            dw[0] = h2f(R.w.w[0] & 0xffff);
+            dw[1] = h2f(R.w.w[8] >> 16);
+        }
+    }
+}
+
+template <int TY, bool GLU>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     constexpr int NW = GLU ? 2 : 1;
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    constexpr int NT = 2;  // 32-token tiles per wave
+    constexpr int QB = GemmLds<TY>::QB, WST = GemmLds<TY>::WST;
+    __shared__ GemmStage<TY, GLU> st[2];
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, l = tid & 63;
+    const int wr = wv >> 1, wc = wv & 1;
     // workgroups of one row group share an XCD (id mod 8) and are dispatched together
     const int bid = blockIdx.x;
     const int xcd = bid & 7, u = bid >> 3;
     const int tg = u % p.n_tg;
     const int rg = (u / p.n_tg) * 8 + xcd;
-    if (rg >= p.n_rg) return;
+    if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
-    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * GEMM_ROWS + wv * 32;
-    const int rows = p.rows[sg];
-    if (row0 >= rows) return;  // no barriers in this kernel: idle waves leave early
+    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * G_BM;
+    const int t0 = tg * G_BN;
     const int h = l >> 5, m = l & 31;
-    const int r = min(row0 + m, rows - 1);
-    const uint8_t *wrow[NW];
-    wrow[0] = p.w[sg] + (size_t)r * p.rb[sg];
-    if constexpr (GLU) wrow[1] = p.w[1] + (size_t)r * p.rb[1];
-    // A rows: token of row m of each 32-token tile
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
-    const int t0 = tg * 32 * NT;
-    const int K = p.K, nb = K >> 5;
-    const int8_t *arow[NT];
-    const float *drow[NT];
+    const int wrow = wr * 32 + m;  // this lane's weight row in the tile (B operand / result column)
+    int arow[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tok = min(t0 + 32 * t + tok_m, p.n_tok - 1);
-        arow[t] = p.qs + (size_t)tok * K + 16 * h;
-        drow[t] = p.d + (size_t)tok * nb;
-    }
+    for (int t = 0; t < NT; t++) arow[t] = wc * 64 + 32 * t + tok_m;
+
     float acc[NW][NT][16];
 #pragma unroll
     for (int a = 0; a < NW; a++)
@@ -137,55 +187,64 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     const v16i zi = {0};
     const v16f zf = {0};
 
-    // software pipeline: the next unit's loads are in flight during this unit's math
-    WUnit<TY> wu[NW], wn[NW];
-    v4i av[NT][2], an[NT][2];
-    float da[NT][2], dn[NT][2];
-    auto load_unit = [&](int b, WUnit<TY> *W, v4i (*A)[2], float (*D)[2]) {
+    float dep[16];
 #pragma unroll
-        for (int a = 0; a < NW; a++) load_wunit<TY>(wrow[a], b, W[a]);
+    for (int v = 0; v < 16; v++) dep[v] = 0.0f;
+    const int n_stages = p.K / (32 * G_KC);
+    StageRegs<TY, GLU> R;
+    stage_load<TY, GLU>(p, sg, row0, t0, 0, tid, R);
+    stage_store<TY, GLU>(st[0], tid, R);
+    __syncthreads();
+    for (int s = 0; s < n_stages; s++) {
+        const bool more = s + 1 < n_stages;
+        if (more) stage_load<TY, GLU>(p, sg, row0, t0, (s + 1) * G_KC, tid, R);
+        const GemmStage<TY, GLU> &S = st[s & 1];
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            A[t][0] = *(const v4i *)(arow[t] + 32 * b);
-            A[t][1] = *(const v4i *)(arow[t] + 32 * b + 32);
-            D[t][0] = drow[t][b];
-            D[t][1] = drow[t][b + 1];
-        }
-    };
-    load_unit(0, wu, av, da);
-    for (int b = 0; b < nb; b += 2) {
-        if (b + 2 < nb) load_unit(b + 2, wn, an, dn);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < G_KC; j++) {
+            v4i bw[NW];
+            float bs[NW];
 #pragma unroll
             for (int a = 0; a < NW; a++) {
-                float dw;
-                const v4i bw = unpack_w<TY>(wu[a], j, h, dw);
-                const float bs = l < 32 ? dw : 0.0f;
+                const uint4 q = *(const uint4 *)(S.wq[a] + wrow * WST + j * QB + (TY == T_Q4_0 ? 0 : 16 * h));
+                if constexpr (TY == T_Q4_0) {
+                    const uint32_t sh = 4u * (uint32_t)h;
+                    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t][j], bw, zi, 0, 0, 0);
-                    const float as = l < 32 ? da[t][j] : 0.0f;
-                    const v16f S = __builtin_amdgcn_mfma_f32_32x32x2f32(as, bs, zf, 0, 0, 0);
+                    for (int i = 0; i < 4; i++) bw[a][i] = (int)((((qq[i] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+                } else {
+                    bw[a] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                }
+                bs[a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
+            }
 #pragma unroll
-                    for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)I[v], S[v], acc[a][t][v]);
+            for (int t = 0; t < NT; t++) {
+                const v4i av0 = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
+                const float as = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
+#pragma unroll
+                for (int a = 0; a < NW; a++) {
+                    // The empty asm makes this tile's A operand depend on the previous
+                    // tile's finished accumulators: one pair of 32×32 results is live
+                    // at a time (the compiler would otherwise issue every MFMA of the
+                    // stage up front and spill); the SIMD's other waves hide latency.
+                    v4i av = av0;
+                    asm volatile("" : "+v"(av) : "v"(dep[0]), "v"(dep[1]), "v"(dep[2]), "v"(dep[3]), "v"(dep[4]), "v"(dep[5]),
+                                 "v"(dep[6]), "v"(dep[7]), "v"(dep[8]), "v"(dep[9]), "v"(dep[10]), "v"(dep[11]), "v"(dep[12]),
+                                 "v"(dep[13]), "v"(dep[14]), "v"(dep[15]));
+                    const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw[a], zi, 0, 0, 0);
+                    const v16f Sc = __builtin_amdgcn_mfma_f32_32x32x2f32(as, bs[a], zf, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)I[v], Sc[v], acc[a][t][v]);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) dep[v] = acc[a][t][v];
                 }
             }
         }
-        if (b + 2 < nb) {
-#pragma unroll
-            for (int a = 0; a < NW; a++) wu[a] = wn[a];
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                av[t][0] = an[t][0];
-                av[t][1] = an[t][1];
-                da[t][0] = dn[t][0];
-                da[t][1] = dn[t][1];
-            }
-        }
+        if (more) stage_store<TY, GLU>(st[(s + 1) & 1], tid, R);
+        __syncthreads();
     }
-    // ---- epilogue: lane holds weight row row0 + m for tokens t0 + 32t + 16h + v ----
-    const int row = row0 + m;
+    // ---- epilogue: lane holds weight row row0 + wrow for tokens t0 + wc·64 + 32t + 16h + v ----
+    const int rows = p.rows[sg];
+    const int row = row0 + wrow;
     if (row >= rows) return;
     float *out = p.out[sg];
     const int ld = p.ld[sg];
@@ -194,13 +253,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int tok = t0 + 32 * t + 16 * h + v;
+            const int tok = t0 + wc * 64 + 32 * t + 16 * h + v;
             if (tok < p.n_tok) {
                 float y = acc[0][t][v];
-                if constexpr (GLU) {
-                    const float g = acc[0][t][v];
-                    y = (p.glu == 2 ? gelu_tanh_f(g) : silu_f(g)) * acc[NW - 1][t][v];
-                }
+                if constexpr (GLU) y = (p.glu == 2 ? gelu_tanh_f(acc[0][t][v]) : silu_f(acc[0][t][v])) * acc[NW - 1][t][v];
                 float *o = out + (size_t)tok * ld + row;
                 if (epi == EPI_ADD) *o += y;
                 else *o = y;
@@ -208,13 +264,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
         }
 }
 
-bool gemm_supported(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % 64 == 0 && K >= 64; }
+bool gemm_supported(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % (32 * G_KC) == 0 && K > 0; }
 
-template <int TY, int NT, bool GLU>
+template <int TY, bool GLU>
 static void launch_t(GemmP p, hipStream_t st) {
-    p.n_tg = (p.n_tok + 32 * NT - 1) / (32 * NT);
+    p.n_tg = (p.n_tok + G_BN - 1) / G_BN;
     const int slots = (p.n_rg + 7) / 8;
-    hipLaunchKernelGGL((gemm_kernel<TY, NT, GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_kernel<TY, GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
 static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }
@@ -222,7 +278,7 @@ static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }
 static void set_groups(GemmP &p, int nseg) {
     int acc = 0;
     for (int i = 0; i < 3; i++) {
-        if (i < nseg) acc += (p.rows[i] + GEMM_ROWS - 1) / GEMM_ROWS;
+        if (i < nseg) acc += (p.rows[i] + G_BM - 1) / G_BM;
         p.rg_end[i] = acc;
     }
     p.n_rg = acc;
@@ -249,8 +305,8 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (ty == T_Q4_0) launch_t<T_Q4_0, 4, false>(p, st);
-    else launch_t<T_Q8_0, 4, false>(p, st);
+    if (ty == T_Q4_0) launch_t<T_Q4_0, false>(p, st);
+    else launch_t<T_Q8_0, false>(p, st);
     return true;
 }
 
@@ -276,8 +332,8 @@ bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, 2, true>(p, st);
-    else launch_t<T_Q8_0, 2, true>(p, st);
+    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, true>(p, st);
+    else launch_t<T_Q8_0, true>(p, st);
     return true;
 }
 

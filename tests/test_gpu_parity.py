@@ -153,7 +153,7 @@ def test_gemm_matches_oracle_rows(oracle, cuda, ty):
     token counts that are not multiples of the 32×32 tiles."""
     import ggml_np as G
     r = oracle.Rng(31 + ty)
-    for k, rows, n_tok in ((64, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130)):
+    for k, rows, n_tok in ((128, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130)):
         w = r.random_weight(ty, rows, k)
         x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
         act = _quant_on_gpu(x, 1, cuda)["dev"]
