@@ -125,7 +125,7 @@ def main():
         "decode_bytes_per_token": tok_bytes,
         "decode_effective_gbs": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9, 1),
         "decode_frac_hbm_roofline": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "gemv_dec_kernel gate+up+SwiGLU (Q4_0 x Q8_0, Q8_0 hidden out)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_dec_kernel gate+up+SwiGLU (RMSNorm+Q8_0 of x in the prologue, Q4_0 x Q8_0, Q8_0 hidden out)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_us, 2)},

@@ -287,13 +287,16 @@ void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8
         int j = i + 1;
         while (j < nseg && act_format(segs[j].w.ty) == fmt) j++;
         const ActQ8 &a = fmt == ACT_Q8K ? actk_ : (act_q8_0 ? *act_q8_0 : act0_);
-        for (int s = i; s < j; s++) {
-            bool done = false;
-            if (n > 8 && gemm_supported(segs[s].w.ty, K)) done = launch_gemm(&segs[s], 1, a, n, K, st_);
-            if (!done && !launch_gemv(&segs[s], (n > 8) ? 1 : j - s, a, d_xn_, n, K, st_))
-                throw Error{E_UNSUPPORTED, std::string("unsupported: matmul of type ") + type_name(segs[s].w.ty)};
-            if (!done && n <= 8) break;  // the single-token/small-batch launch took the whole run
+        // prompt batches: one GEMM launch per run of segments of one weight type
+        int s = i;
+        while (n > 8 && s < j && gemm_supported(segs[s].w.ty, K)) {
+            int e = s + 1;
+            while (e < j && e - s < 3 && segs[e].w.ty == segs[s].w.ty) e++;
+            if (!launch_gemm(&segs[s], e - s, a, n, K, st_)) break;
+            s = e;
         }
+        if (s < j && !launch_gemv(&segs[s], j - s, a, d_xn_, n, K, st_))
+            throw Error{E_UNSUPPORTED, std::string("unsupported: matmul of type ") + type_name(segs[s].w.ty)};
         i = j;
     }
     check_launch("matmul");
@@ -303,8 +306,13 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     const ModelConfig &c = m_.cfg;
     const int E = (int)c.n_embd, ff = (int)L.ff;
     const DevWeight *ws[2] = {&L.gate, &L.up};
-    prepare(d_x_, L.ffn_norm, n, E, ws, 2, false);
-    mark("rmsnorm_quant");
+    // single token with Q4_0/Q8_0 gate/up: the gate/up kernel normalizes x itself
+    const bool self_norm = n == 1 && !capture_ && L.ffn_norm && L.gate.ty == L.up.ty && gemv_norm_ok(L.gate.ty, E);
+    const NormIn nin{d_x_, L.ffn_norm, c.rms_eps};
+    if (!self_norm) {
+        prepare(d_x_, L.ffn_norm, n, E, ws, 2, false);
+        mark("rmsnorm_quant");
+    }
     const ActQ8 &a = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
     bool done = false;
     if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
@@ -312,8 +320,8 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     // single-token Q8_0 down projection: the gate/up kernel quantizes h itself
     bool h_quantized = false;
     if (!done && n == 1 && fmt == ACT_Q8_0 && ff % 32 == 0)
-        h_quantized = done = launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, &act_h_, st_);
-    if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, nullptr, st_))
+        h_quantized = done = launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, &act_h_, st_, self_norm ? &nin : nullptr);
+    if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, n, E, d_h_, ff, c.gelu, nullptr, st_, self_norm ? &nin : nullptr))
         throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
     check_launch("ffn glu");
     mark("matmul_gate_up_glu");
@@ -338,10 +346,21 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         const bool swa = c.is_swa(il);
         // ---- attention block ----
         const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
-        prepare(d_x_, L.attn_norm, n, E, ws, 3, false);
-        mark("rmsnorm_quant");
+        // single token with Q4_0/Q8_0 Q/K/V: the GEMV normalizes x itself
+        const bool self_norm = n == 1 && !capture_ && L.attn_norm && gemv_norm_ok(L.wq.ty, E) && gemv_norm_ok(L.wk.ty, E) &&
+                               gemv_norm_ok(L.wv.ty, E);
+        const NormIn nin{d_x_, L.attn_norm, c.rms_eps};
+        if (!self_norm) {
+            prepare(d_x_, L.attn_norm, n, E, ws, 3, false);
+            mark("rmsnorm_quant");
+        }
         GemvSeg qkv[3] = {{L.wq, d_q_, qd, EPI_STORE}, {L.wk, d_k_, kvd, EPI_STORE}, {L.wv, d_v_, kvd, EPI_STORE}};
-        matmul(qkv, 3, n, E);
+        if (self_norm) {
+            if (!launch_gemv(qkv, 3, act0_, d_xn_, n, E, st_, &nin)) throw rt_err("normalizing Q/K/V GEMV launch failed");
+            check_launch("matmul");
+        } else {
+            matmul(qkv, 3, n, E);
+        }
         mark("matmul_qkv");
         if (capture_ && !in_capture_) {
             RIE_HIP_CHECK(hipStreamSynchronize(st_));
@@ -641,14 +660,18 @@ double HipBackend::time_ffn_glu(int reps, size_t *bytes) {
     auto one_pass = [&](size_t *b) {
         for (const auto &L : layers_) {
             const int ff = (int)L.ff;
+            // the same launch as a decode step (ffn_dense)
+            const bool self_norm = L.ffn_norm && L.gate.ty == L.up.ty && gemv_norm_ok(L.gate.ty, E);
+            const NormIn nin{d_x_, L.ffn_norm, c.rms_eps};
             const bool hq = act_format(L.down.ty) == ACT_Q8_0 && ff % 32 == 0;
-            bool done = hq && launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, &act_h_, st_);
-            if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, nullptr, st_))
+            bool done = hq && launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, &act_h_, st_, self_norm ? &nin : nullptr);
+            if (!done && !launch_gemv_glu(L.gate, L.up, a, d_xn_, 1, E, d_h_, ff, c.gelu, nullptr, st_, self_norm ? &nin : nullptr))
                 throw Error{E_UNSUPPORTED, "unsupported: gated FFN weights"};
             if (b && !*b) {  // weights + activation read + hidden (and its Q8_0) written
-                size_t in = fmt_in == ACT_F32 ? (size_t)E * 4
-                                              : fmt_in == ACT_Q8_0 ? (size_t)E + (size_t)E / 32 * (L.gate.ty == T_Q4_0 ? 8 : 4)
-                                                                   : (size_t)E + (size_t)E / 256 * 4 + (size_t)E / 16 * 2;
+                size_t in = self_norm ? (size_t)E * 8  // residual row and norm weight, f32
+                            : fmt_in == ACT_F32 ? (size_t)E * 4
+                            : fmt_in == ACT_Q8_0 ? (size_t)E + (size_t)E / 32 * (L.gate.ty == T_Q4_0 ? 8 : 4)
+                                                 : (size_t)E + (size_t)E / 256 * 4 + (size_t)E / 16 * 2;
                 *b = L.gate.rows * L.gate.rb() + L.up.rows * L.up.rb() + in + (size_t)ff * 4 + (done ? (size_t)ff + (size_t)ff / 32 * 12 : 0);
             }
         }

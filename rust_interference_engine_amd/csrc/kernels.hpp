@@ -23,12 +23,21 @@ struct GemvSeg {
 };
 // y_seg = W_seg · act for up to 3 segments sharing one activation batch (n_tok rows).
 // Returns false when a weight type/shape has no kernel.
-bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st);
+// nin (single token, Q4_0/Q8_0 weights, K ≤ 4096): the kernel computes the
+// activation itself as Q8_0(RMSNorm(x)·w) — no separate normalization launch.
+struct NormIn {
+    const float *x;   // residual row [K]
+    const float *w;   // norm weight [K]
+    float eps;
+};
+bool gemv_norm_ok(int ty, size_t K);
+bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
+                 const NormIn *nin = nullptr);
 // h = act(gate·x) ⊙ (up·x) for gated feed-forward blocks (gelu selects GELU-tanh).
 // hq (n_tok == 1, Q8_0 down projection): also quantize h to Q8_0 in the epilogue;
 // returns false (nothing launched) when that is not possible.
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
-                     int ld, int gelu, const ActQ8 *hq, hipStream_t st);
+                     int ld, int gelu, const ActQ8 *hq, hipStream_t st, const NormIn *nin = nullptr);
 bool gemv_supported(int ty, size_t K);
 
 // ---- attention.hip ----

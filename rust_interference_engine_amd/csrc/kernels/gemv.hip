@@ -291,6 +291,7 @@ struct DecP {
     const float *actf;
     int glu;         // 0 none, 1 silu, 2 gelu
     ActQ8 hq;        // GLU: Q8_0 output of h when hq.qs != nullptr
+    NormIn nin;      // nin.x != nullptr: the activation is RMSNorm(x)·w, quantized here
 };
 
 template <int TY>
@@ -497,7 +498,6 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     for (int k = 0; k < UPL; k++) {
         valid[k] = l + LPR * k < U;
         uu[k] = valid[k] ? l + LPR * k : U - 1;  // idle lanes load a real unit and drop it
-        if (valid[k]) load_act<TY>(a[k], uu[k], p.act, p.actf, p.K);
     }
     // workgroup → (segment, first row): uniform, so the segment's fields are scalar
     const int bid = blockIdx.x;
@@ -507,8 +507,8 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     const int last = seg_rows - 1;
     const uint8_t *wbase = p.seg[sg].w;
     const size_t rb = p.seg[sg].rb;
-    for (int base = grp * R; base < p.tr; base += GROUPS * R) {
-        Raw<TY> raw[NW][R][UPL];
+    Raw<TY> raw[NW][R][UPL];
+    auto load_pass = [&](int base) {
 #pragma unroll
         for (int k = 0; k < R; k++) {
             const int r = min(row0 + base + k, last);
@@ -521,6 +521,102 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
                 for (int u = 0; u < UPL; u++) load_raw<TY>(row2, uu[u], raw[1][k][u]);
             }
         }
+    };
+    const int base0 = grp * R;
+    if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
+    bool have_act = false;
+    if constexpr (TY == T_Q4_0 || TY == T_Q8_0) {
+        if (p.nin.x) {
+            // The activation is Q8_0(RMSNorm(x)·w), made here once per workgroup:
+            // thread τ normalizes values 16τ..16τ+15 (a 32-block is a thread pair)
+            // into LDS, then every lane reads its slice (quantizer: quant.hip).
+            __shared__ __align__(16) int8_t s_q[4096];
+            __shared__ float s_d[128], s_red[4];
+            __shared__ int s_i[128];
+            const int K = p.K, nthr = K >> 4;
+            const bool act = tid < nthr;
+            float4 xv[4], gv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = gv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float ss = 0.0f;
+            if (act) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    xv[i] = ((const float4 *)(p.nin.x + 16 * tid))[i];
+                    gv[i] = ((const float4 *)(p.nin.w + 16 * tid))[i];
+                    ss = fmaf(xv[i].x, xv[i].x, ss);
+                    ss = fmaf(xv[i].y, xv[i].y, ss);
+                    ss = fmaf(xv[i].z, xv[i].z, ss);
+                    ss = fmaf(xv[i].w, xv[i].w, ss);
+                }
+            }
+            ss = wave_sum(ss, 64);
+            if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+            __syncthreads();
+            const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+            float y[16];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                y[4 * i] = xv[i].x * scale * gv[i].x;
+                y[4 * i + 1] = xv[i].y * scale * gv[i].y;
+                y[4 * i + 2] = xv[i].z * scale * gv[i].z;
+                y[4 * i + 3] = xv[i].w * scale * gv[i].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(y[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            uint32_t w4[4];
+            int isum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    int q = (int)rintf(y[4 * j + e] * id);
+                    q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                    isum += q;
+                    v |= ((uint32_t)(q & 0xff)) << (8 * e);
+                }
+                w4[j] = v;
+            }
+            isum += __shfl_xor(isum, 1, 64);
+            if (act) {
+                *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                if ((tid & 1) == 0) {
+                    s_d[tid >> 1] = d;
+                    s_i[tid >> 1] = isum;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const uint4 *src = (const uint4 *)(s_q + 64 * uu[k]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint4 v = src[i];
+                    a[k].q[4 * i] = v.x;
+                    a[k].q[4 * i + 1] = v.y;
+                    a[k].q[4 * i + 2] = v.z;
+                    a[k].q[4 * i + 3] = v.w;
+                }
+                a[k].d0 = s_d[2 * uu[k]];
+                a[k].d1 = s_d[2 * uu[k] + 1];
+                a[k].i0 = s_i[2 * uu[k]];
+                a[k].i1 = s_i[2 * uu[k] + 1];
+            }
+            have_act = true;
+        }
+    }
+    if (!have_act) {
+#pragma unroll
+        for (int k = 0; k < UPL; k++)
+            if (valid[k]) load_act<TY>(a[k], uu[k], p.act, p.actf, p.K);
+    }
+    for (int base = base0; base < p.tr; base += GROUPS * R) {
+        if (base != base0) load_pass(base);
 #pragma unroll
         for (int wv = 0; wv < NW; wv++)
 #pragma unroll
@@ -710,8 +806,14 @@ static bool operands_ok(int ty, const ActQ8 &act, const float *act_f32) {
     }
 }
 
-bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st) {
+bool gemv_norm_ok(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % 64 == 0 && K >= 64 && K <= 4096; }
+
+bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
+                 const NormIn *nin) {
     if (n_tok < 1) return false;
+    if (nin && (n_tok != 1 || !nin->x || !nin->w)) return false;
+    for (int s = 0; s < nseg; s++)
+        if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K)) return false;
     // segments of one launch must share a weight type; split otherwise
     int i = 0;
     while (i < nseg) {
@@ -741,16 +843,18 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
             d.K = K;
             d.act = act;
             d.actf = act_f32;
+            if (nin) d.nin = *nin;
             done = dispatch_dec(segs[i].w.ty, d, st);
         }
-        if (!done && !dispatch(segs[i].w.ty, p, st)) return false;
+        if (!done && (nin || !dispatch(segs[i].w.ty, p, st))) return false;
         i = j;
     }
     return true;
 }
 
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
-                     int ld, int gelu, const ActQ8 *hq, hipStream_t st) {
+                     int ld, int gelu, const ActQ8 *hq, hipStream_t st, const NormIn *nin) {
+    if (nin && (n_tok != 1 || !nin->x || !nin->w || !gemv_norm_ok(gate.ty, (size_t)K))) return false;
     if (gate.ty != up.ty || gate.rows != up.rows || !gemv_supported(gate.ty, K) || gate.cols != (size_t)K || up.cols != (size_t)K ||
         !gate.data || !up.data || !h || n_tok < 1 || !operands_ok(gate.ty, act, act_f32))
         return false;
@@ -775,9 +879,10 @@ bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
         d.actf = act_f32;
         d.glu = p.glu;
         if (hq) d.hq = *hq;
+        if (nin) d.nin = *nin;
         if (dispatch_dec(gate.ty, d, st)) return true;
     }
-    if (hq) return false;  // the batched kernel does not quantize h
+    if (hq || nin) return false;  // the batched kernel neither quantizes h nor normalizes
     return dispatch(gate.ty, p, st);
 }
 

@@ -12,126 +12,29 @@
 #include "../common.hpp"
 #include "../device.hpp"
 #include "../kernels.hpp"
+#include "../norm_quant.hpp"
 
 namespace rie {
 
 // Grid (row chunks, rows): every workgroup recomputes its row's sum of squares
-// (the row is L2-resident) and quantizes QB8 blocks of 32 (Q8_0: 8 per
-// iteration, one per half-wave) or 4 blocks of 256 (Q8_K: one per wave).
+// (the row is L2-resident) and quantizes its chunk: 16 Q8_0 blocks (two per
+// wave) or 4 Q8_K blocks (one per wave).
 constexpr int Q8_0_BLOCKS_PER_WG = 16;
 constexpr int Q8K_BLOCKS_PER_WG = 4;
 
 template <int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w,
                                                             float eps, int E, float *__restrict__ xn, ActQ8 act) {
-    const int row = blockIdx.y;
-    const int tid = threadIdx.x;
-    const float *xr = x + (size_t)row * ldx;
     __shared__ float red[4];
-    __shared__ float s_scale;
-    float scale = 1.0f;
-    if (w) {
-        float ss = 0.0f;
-        for (int i = tid * 4; i < E; i += 1024) {
-            const float4 v = *(const float4 *)(xr + i);
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
-        }
-        ss = wave_sum(ss, 64);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        if (tid == 0) {
-            float t = (red[0] + red[1]) + (red[2] + red[3]);
-            s_scale = 1.0f / sqrtf(t / (float)E + eps);
-        }
-        __syncthreads();
-        scale = s_scale;
-    }
+    const int row = blockIdx.y;
+    const float *xr = x + (size_t)row * ldx;
+    const float scale = w ? rms_scale_wg(xr, E, eps, red) : 1.0f;
     if (FMT == ACT_Q8_0) {
-        const int hw = tid >> 5, j = tid & 31;
-        const int nb = E >> 5;
         const int b0 = blockIdx.x * Q8_0_BLOCKS_PER_WG;
-        for (int b = b0 + hw; b < min(nb, b0 + Q8_0_BLOCKS_PER_WG); b += 8) {
-            const int i = (b << 5) + j;
-            float y = w ? xr[i] * scale * w[i] : xr[i];
-            if (xn) xn[(size_t)row * E + i] = y;
-            float amax = fabsf(y);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            const int q = (int)rintf(y * id);
-            const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
-            int su = q, sc = qc;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) {
-                su += __shfl_xor(su, o, 64);
-                sc += __shfl_xor(sc, o, 64);
-            }
-            act.qs[(size_t)row * E + i] = (int8_t)qc;
-            if (j == 0) {
-                const size_t bi = (size_t)row * nb + b;
-                act.d[bi] = d;
-                if (act.s) act.s[bi] = d * (float)su;
-                if (act.isum) act.isum[bi] = sc;
-            }
-        }
+        quant_q8_0_range(xr, w, scale, E, xn, act, row, b0, min(E >> 5, b0 + Q8_0_BLOCKS_PER_WG));
     } else {
-        const int wv = tid >> 6, l = tid & 63;
-        const int nb = E >> 8;
-        const int b = blockIdx.x * Q8K_BLOCKS_PER_WG + wv;
-        if (b < nb) {
-            const int i0 = (b << 8) + (l << 2);
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                y[e] = w ? xr[i0 + e] * scale * w[i0 + e] : xr[i0 + e];
-                if (xn) xn[(size_t)row * E + i0 + e] = y[e];
-            }
-            float amax = 0.0f, mx = 0.0f;
-            int idx = 0x7fffffff;
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (fabsf(y[e]) > amax) {
-                    amax = fabsf(y[e]);
-                    mx = y[e];
-                    idx = (l << 2) + e;
-                }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                float oa = __shfl_xor(amax, o, 64), om = __shfl_xor(mx, o, 64);
-                int oi = __shfl_xor(idx, o, 64);
-                if (oa > amax || (oa == amax && oi < idx)) {
-                    amax = oa;
-                    mx = om;
-                    idx = oi;
-                }
-            }
-            int8_t *qo = act.qs + (size_t)row * E + i0;
-            const size_t bi = (size_t)row * nb + b;
-            if (amax == 0.0f) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) qo[e] = 0;
-                if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = 0;
-                if (l == 0) act.d[bi] = 0.0f;
-            } else {
-                const float iscale = -127.0f / mx;
-                int s4 = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    int q = (int)roundf(iscale * y[e]);
-                    q = q < -127 ? -127 : (q > 127 ? 127 : q);
-                    qo[e] = (int8_t)q;
-                    s4 += q;
-                }
-                s4 += __shfl_xor(s4, 1, 64);
-                s4 += __shfl_xor(s4, 2, 64);
-                if ((l & 3) == 0) act.bsums[(size_t)row * (E >> 4) + (b << 4) + (l >> 2)] = (int16_t)s4;
-                if (l == 0) act.d[bi] = 1.0f / iscale;
-            }
-        }
+        const int b0 = blockIdx.x * Q8K_BLOCKS_PER_WG;
+        quant_q8k_range(xr, w, scale, E, xn, act, row, b0, min(E >> 8, b0 + Q8K_BLOCKS_PER_WG));
     }
 }
 
