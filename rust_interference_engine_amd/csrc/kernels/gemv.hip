@@ -480,10 +480,9 @@ constexpr int dec_rows_per_pass() { return (TY == T_Q8_0 || TY == T_Q6_K || TY =
 
 constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 
-template <int TY, int LPR, int UPL, bool GLU>
+template <int TY, int LPR, int UPL, bool GLU, int R>
 __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     constexpr int GROUPS = 256 / LPR;
-    constexpr int R = dec_rows_per_pass<TY>();
     constexpr int STRIDE = LPR + DEC_PAD;
     constexpr int NW = GLU ? 2 : 1;
     extern __shared__ float red[];  // [NW][tr][STRIDE], then tr floats of h
@@ -698,9 +697,19 @@ static int dec_tile_override() {
     return v;
 }
 
-template <int TY>
-static bool launch_dec_t(DecP p, hipStream_t st) {
-    constexpr int R = dec_rows_per_pass<TY>();
+// Rows per pass override for Q4_0 (tuning): 0 default, 1 eight rows for the
+// gate/up kernel with the Q8_0 hidden, 2 eight rows for every Q4_0 launch.
+static int dec_r8_mode() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RIE_HIP_DEC_R8");
+        v = e ? atoi(e) : 0;
+    }
+    return v;
+}
+
+template <int TY, int R>
+static bool launch_dec_r(DecP p, hipStream_t st) {
     const int U = dec_units(TY, p.K);
     int lpr = 16;
     while (lpr < U && lpr < 256) lpr *= 2;
@@ -726,8 +735,8 @@ static bool launch_dec_t(DecP p, hipStream_t st) {
     }
 #define RIE_DEC(L, UP)                                                                        \
     do {                                                                                      \
-        if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true>), dim3(blocks), dim3(256), lds, st, p);  \
-        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false>), dim3(blocks), dim3(256), lds, st, p);       \
+        if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R>), dim3(blocks), dim3(256), lds, st, p);  \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R>), dim3(blocks), dim3(256), lds, st, p);       \
     } while (0)
     if (upl == 1) {
         switch (lpr) {
@@ -742,6 +751,15 @@ static bool launch_dec_t(DecP p, hipStream_t st) {
     }
 #undef RIE_DEC
     return true;
+}
+
+template <int TY>
+static bool launch_dec_t(const DecP &p, hipStream_t st) {
+    if constexpr (TY == T_Q4_0) {
+        const int m = dec_r8_mode();
+        if (m == 2 || (m == 1 && p.glu && p.hq.qs)) return launch_dec_r<TY, 8>(p, st);
+    }
+    return launch_dec_r<TY, dec_rows_per_pass<TY>()>(p, st);
 }
 
 static bool dispatch_dec(int ty, const DecP &p, hipStream_t st) {
