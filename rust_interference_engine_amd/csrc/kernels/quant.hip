@@ -97,6 +97,69 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t *__restrict__
         y = (float)(int8_t)b[2 + (i & 31)] * h2f(b[0] | (b[1] << 8));
         break;
     }
+    case T_BF16: y = __uint_as_float((uint32_t)((const uint16_t *)row)[i] << 16); break;
+    case T_Q4_1: {
+        const uint8_t *b = row + (i >> 5) * 20;
+        const int j = i & 31;
+        const int q = j < 16 ? (b[4 + j] & 15) : (b[4 + j - 16] >> 4);
+        y = (float)q * h2f(b[0] | (b[1] << 8)) + h2f(b[2] | (b[3] << 8));
+        break;
+    }
+    case T_Q5_0:
+    case T_Q5_1: {
+        const bool m = ty == T_Q5_1;
+        const uint8_t *b = row + (i >> 5) * (m ? 24 : 22);
+        const int j = i & 31;
+        const uint8_t *hq = b + (m ? 4 : 2);
+        const uint32_t qh = hq[0] | (hq[1] << 8) | (hq[2] << 16) | ((uint32_t)hq[3] << 24);
+        const uint8_t *qs = hq + 4;
+        const int lo = j < 16 ? (qs[j] & 15) : (qs[j - 16] >> 4);
+        const int q = lo | (((qh >> j) & 1) << 4);
+        const float d = h2f(b[0] | (b[1] << 8));
+        y = m ? (float)q * d + h2f(b[2] | (b[3] << 8)) : (float)(q - 16) * d;
+        break;
+    }
+    case T_Q2_K: {
+        const uint8_t *b = row + (i >> 8) * 84;
+        const int r = i & 255, n = r >> 7, js = (r >> 5) & 3, half = (r >> 4) & 1, l = r & 15;
+        const uint8_t sc = b[8 * n + 2 * js + half];
+        const int q = (b[16 + 32 * n + l + 16 * half] >> (2 * js)) & 3;
+        const float d = h2f(b[80] | (b[81] << 8)), mn = h2f(b[82] | (b[83] << 8));
+        y = d * (float)(sc & 0xF) * (float)q - mn * (float)(sc >> 4);
+        break;
+    }
+    case T_Q3_K: {
+        const uint8_t *b = row + (i >> 8) * 110;
+        const int r = i & 255, n = r >> 7, js = (r >> 5) & 3, half = (r >> 4) & 1, l = r & 15;
+        const int idx = l + 16 * half, is = 8 * n + 2 * js + half;
+        const int v = ((b[32 + 32 * n + idx] >> (2 * js)) & 3) - ((b[idx] >> (4 * n + js)) & 1 ? 0 : 4);
+        // 6-bit scale `is` (unpack_q3k_scales): low 4 bits from bytes 0..7, high 2 bits from bytes 8..11
+        const int lo4 = is < 8 ? (b[96 + is] & 0xF) : (b[96 + is - 8] >> 4);
+        const int hi2 = (b[96 + 8 + (is & 3)] >> (2 * (is >> 2))) & 3;
+        const int sc = (lo4 | (hi2 << 4)) - 32;
+        y = h2f(b[108] | (b[109] << 8)) * (float)sc * (float)v;
+        break;
+    }
+    case T_Q5_K: {
+        const uint8_t *b = row + (i >> 8) * 176;
+        const int r = i & 255, j = r >> 6, l = r & 63;
+        const float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        const uint8_t *q = b + 4;
+        const int sj = 2 * j + (l >= 32);
+        uint8_t sc, mn;
+        if (sj < 4) {
+            sc = q[sj] & 63;
+            mn = q[sj + 4] & 63;
+        } else {
+            sc = (q[sj + 4] & 0xF) | ((q[sj - 4] >> 6) << 4);
+            mn = (q[sj + 4] >> 4) | ((q[sj] >> 6) << 4);
+        }
+        const uint8_t ql = b[48 + 32 * j + (l & 31)];
+        const int hbit = (b[16 + (l & 31)] >> (2 * j + (l >= 32))) & 1;
+        const int v = (l < 32 ? (ql & 15) : (ql >> 4)) + 16 * hbit;
+        y = d * (float)sc * (float)v - dmin * (float)mn;
+        break;
+    }
     case T_Q4_K: {
         const uint8_t *b = row + (i >> 8) * 144;
         const int r = i & 255, j = r >> 6, l = r & 63;

@@ -17,6 +17,13 @@ import rust_interference_engine_amd as R  # noqa: E402
 from rust_interference_engine_amd import synth  # noqa: E402
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, BF16 = 3, 6, 7, 10, 11, 13, 30
+ALL_TYPES = [Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, F32, F16, BF16]
+
+
+def act_fmt(ty):
+    """activation format a weight type consumes (quant/mod.rs:118-124): 0 f32, 1 Q8_0, 2 Q8_K"""
+    return 0 if ty in (F32, F16, BF16) else (2 if ty in (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) else 1)
 
 
 @pytest.fixture(scope="module")
@@ -126,7 +133,7 @@ def _gemv(ty, w, rows, k, act, act_f32, n_tok, cuda, gemm=False):
     return host(out).reshape(n_tok, rows)
 
 
-@pytest.mark.parametrize("ty", [Q4_0, Q8_0, Q4_K, Q6_K, F32, F16])
+@pytest.mark.parametrize("ty", ALL_TYPES)
 def test_gemv_matches_oracle_rows(oracle, cuda, ty):
     import ggml_np as G
     r = oracle.Rng(21 + ty)
@@ -135,7 +142,7 @@ def test_gemv_matches_oracle_rows(oracle, cuda, ty):
         w = r.random_weight(ty, rows, k)
         for n_tok in (1, 3, 6):
             x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
-            fmt = 0 if ty in (F32, F16) else (2 if ty in (Q4_K, Q6_K) else 1)
+            fmt = act_fmt(ty)
             act = _quant_on_gpu(x, fmt, cuda)["dev"] if fmt else None
             got = _gemv(ty, w, rows, k, act, x if fmt == 0 else None, n_tok, cuda)
             wf = G.dequantize(ty, w, rows * k).reshape(rows, k).astype(np.float64)
@@ -234,6 +241,8 @@ CASES = [
     ("llama", F16, 0, 3e-3), ("llama", F32, 0, 3e-3), ("qwen3", Q4_0, 0, 0.03), ("qwen2", Q4_0, 0, 0.03),
     ("gemma3", Q4_0, 0, 0.03), ("granite", F16, 0, 3e-3), ("phi3", Q4_0, 0, 0.03), ("gemma2", F16, 0, 3e-3),
     ("llama", Q4_0, 1, 0.05), ("llama", Q4_0, 2, 0.05), ("qwen3", Q4_K, 2, 0.05),
+    ("llama", Q4_1, 0, 0.03), ("llama", Q5_0, 0, 0.03), ("llama", Q5_1, 0, 0.03), ("llama", Q2_K, 0, 0.03),
+    ("llama", Q3_K, 0, 0.03), ("llama", Q5_K, 0, 0.03), ("llama", BF16, 0, 3e-3),
 ]
 
 
