@@ -56,7 +56,11 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     for (auto &L : m_.layers) {
         need(L.wq, "attn_q"); need(L.wk, "attn_k"); need(L.wv, "attn_v"); need(L.wo, "attn_output");
         need(L.gate, "ffn_gate"); need(L.up, "ffn_up"); need(L.down, "ffn_down"); need(L.router, "ffn_gate_inp");
-        if (L.moe && L.shexp_gate.present()) throw Error{E_UNSUPPORTED, "unsupported: shared experts on the HIP backend"};
+        if (L.moe) {
+            need(L.shexp_gate, "ffn_gate_shexp"); need(L.shexp_up, "ffn_up_shexp"); need(L.shexp_down, "ffn_down_shexp");
+            if (m_.cfg.n_expert > 512 || L.n_used > 64)
+                throw Error{E_UNSUPPORTED, "unsupported: more than 512 experts or 64 experts per token on the HIP backend"};
+        }
         for (const HostWeight *nw : {&L.attn_norm, &L.ffn_norm, &L.q_norm, &L.k_norm, &L.bq, &L.bk, &L.bv, &L.post_attn_norm, &L.post_ffn_norm})
             if (nw->present() && nw->ty != T_F32) throw Error{E_UNSUPPORTED, "unsupported: non-F32 norm/bias vectors"};
     }
@@ -101,6 +105,12 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         D.moe = L.moe;
         if (L.moe) {
             D.router = dev(L.router);
+            if (L.shexp_gate.present()) {
+                D.sh_gate = dev(L.shexp_gate);
+                D.sh_up = dev(L.shexp_up);
+                D.sh_down = dev(L.shexp_down);
+            }
+            D.sh_gate_inp = dev_vec(L.shexp_gate_inp);
             D.n_used = L.n_used;
             D.ff = c.n_ff_exp;
             D.norm_topk = L.norm_topk;
@@ -196,10 +206,11 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     act0_.isum = dalloc<int32_t>(allocs_, kq / 32);
     // Q8_0 of the single-token FFN hidden, written by the gate/up kernel while
     // it still reads act0_
-    act_h_.qs = dalloc<int8_t>(allocs_, ff_max_);
-    act_h_.d = dalloc<float>(allocs_, ff_max_ / 32 + 1);
-    act_h_.s = dalloc<float>(allocs_, ff_max_ / 32 + 1);
-    act_h_.isum = dalloc<int32_t>(allocs_, ff_max_ / 32 + 1);
+    const size_t hrows = c.n_expert ? c.n_expert_used : 1;  // routed experts of one token
+    act_h_.qs = dalloc<int8_t>(allocs_, hrows * ff_max_);
+    act_h_.d = dalloc<float>(allocs_, hrows * ff_max_ / 32 + 1);
+    act_h_.s = dalloc<float>(allocs_, hrows * ff_max_ / 32 + 1);
+    act_h_.isum = dalloc<int32_t>(allocs_, hrows * ff_max_ / 32 + 1);
     actk_.qs = dalloc<int8_t>(allocs_, kq);
     actk_.d = dalloc<float>(allocs_, kq / 256 + 1);
     actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
@@ -211,6 +222,12 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         d_router_ = dalloc<float>(allocs_, mb * c.n_expert);
         d_moe_w_ = dalloc<float>(allocs_, mb * c.n_expert_used);
         d_moe_sel_ = dalloc<int>(allocs_, mb * c.n_expert_used);
+        d_moe_y_ = dalloc<float>(allocs_, mb * c.n_expert_used * E);
+        d_moe_xn_ = dalloc<float>(allocs_, mb * E);
+        d_moe_xg_ = dalloc<float>(allocs_, mb * E);
+        d_moe_yg_ = dalloc<float>(allocs_, mb * E);
+        d_moe_rows_ = dalloc<int>(allocs_, mb * c.n_expert_used);
+        d_moe_rw_ = dalloc<float>(allocs_, mb * c.n_expert_used);
     }
     cap_.resize(7);
     RIE_HIP_CHECK(hipDeviceSynchronize());
@@ -442,6 +459,8 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         const bool fdirect = !L.post_ffn_norm && c.residual_scale == 1.0f;
         if (L.moe) {
             ffn_moe(L, n);
+            if (L.post_ffn_norm) launch_rmsnorm(d_o_, E, L.post_ffn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);
+            launch_add_inplace(d_x_, d_o_, (size_t)n * E, c.residual_scale, st_);
         } else {
             ffn_dense(L, n, fdirect ? d_x_ : d_o_, fdirect ? EPI_ADD : EPI_STORE);
             if (capture_ && !in_capture_) {
@@ -491,10 +510,108 @@ void HipBackend::head(int first, int m) {
     check_launch("head");
 }
 
+static DevWeight slice_rows(const DevWeight &w, size_t r0, size_t rows) {
+    DevWeight s = w;
+    s.data = w.data + r0 * w.rb();
+    s.rows = rows;
+    return s;
+}
+
+// y = down(act(gate·x) ⊙ up·x) for m rows of x (dense_ffn, cpu.rs:431-467); x is
+// already normalized, so the activations are only quantized.
+void HipBackend::expert_ffn(const DevWeight &g, const DevWeight &u, const DevWeight &dn, const float *x, int m, float *y) {
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd, ff = (int)g.rows;
+    const DevWeight *ws[2] = {&g, &u};
+    prepare(x, nullptr, m, E, ws, 2, false);
+    const ActQ8 &a = act_format(g.ty) == ACT_Q8K ? actk_ : act0_;
+    bool done = false;
+    if (m > 8 && gemm_supported(g.ty, E)) done = launch_gemm_glu(g, u, a, m, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
+    if (!done && !launch_gemv_glu(g, u, a, d_xn_, m, E, d_h_, ff, c.gelu, nullptr, st_))
+        throw Error{E_UNSUPPORTED, "unsupported: expert FFN weights"};
+    const int fmt = act_format(dn.ty);
+    if (fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_h_, (size_t)m * ff * 4, hipMemcpyDeviceToDevice, st_));
+    else launch_quant_only(d_h_, ff, m, ff, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+    GemvSeg s{dn, y, E, EPI_STORE};
+    matmul(&s, 1, m, ff);
+}
+
+// moe_ffn (cpu.rs:469-524): router logits → softmax/top-k (on the device) → the
+// routed experts' outputs weighted and summed in ascending expert order into
+// d_o_, plus the optionally gated shared expert.  One token: everything stays on
+// the device (graph replay); prompt batches read the routing back and run each
+// selected expert once over its gathered tokens.
 void HipBackend::ffn_moe(const DevLayer &L, int n) {
-    (void)L;
-    (void)n;
-    throw Error{E_UNSUPPORTED, "unsupported: mixture-of-experts layers on the HIP backend"};
+    const ModelConfig &c = m_.cfg;
+    const int E = (int)c.n_embd, ne = (int)c.n_expert, k = (int)L.n_used, ff = (int)L.ff;
+    const bool shared = L.sh_gate.data != nullptr;
+    const DevWeight *ws[4] = {&L.router, &L.gate, &L.up, shared ? &L.sh_gate : nullptr};
+    prepare(d_x_, L.ffn_norm, n, E, ws, 4, true);  // f32 rows for the router, gathers and the shared gate
+    mark("rmsnorm_quant");
+    GemvSeg rs{L.router, d_router_, ne, EPI_STORE};
+    matmul(&rs, 1, n, E);
+    launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
+    check_launch("moe route");
+    mark("moe_route");
+    RIE_HIP_CHECK(hipMemcpyAsync(d_moe_xn_, d_xn_, (size_t)n * E * 4, hipMemcpyDeviceToDevice, st_));
+    if (n == 1) {
+        const ActQ8 &ax = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
+        const int dfmt = act_format(L.down.ty);
+        bool hq = dfmt == ACT_Q8_0 && ff % 32 == 0 &&
+                  launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, &act_h_, st_);
+        if (!hq && !launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, nullptr, st_))
+            throw Error{E_UNSUPPORTED, "unsupported: routed expert weights"};
+        mark("moe_gate_up_glu");
+        if (!hq && dfmt != ACT_F32) launch_quant_only(d_h_, ff, k, ff, dfmt, dfmt == ACT_Q8K ? actk_ : act0_, st_);
+        const ActQ8 &ah = hq ? act_h_ : (dfmt == ACT_Q8K ? actk_ : act0_);
+        if (!launch_gemv_experts(L.down, E, d_moe_sel_, k, ah, d_h_, true, ff, d_moe_y_, st_))
+            throw Error{E_UNSUPPORTED, "unsupported: routed expert down weights"};
+        mark("moe_down");
+        launch_moe_combine(d_moe_y_, d_moe_w_, 1, k, E, d_o_, EPI_STORE, st_);
+    } else {
+        std::vector<int> sel((size_t)n * k);
+        std::vector<float> w((size_t)n * k);
+        RIE_HIP_CHECK(hipMemcpyAsync(sel.data(), d_moe_sel_, sel.size() * 4, hipMemcpyDeviceToHost, st_));
+        RIE_HIP_CHECK(hipMemcpyAsync(w.data(), d_moe_w_, w.size() * 4, hipMemcpyDeviceToHost, st_));
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        // tokens of each expert, experts in ascending order (cpu.rs:489-501)
+        std::vector<std::vector<std::pair<int, float>>> assign(ne);
+        for (int t = 0; t < n; t++)
+            for (int j = 0; j < k; j++) {
+                const int ex = sel[(size_t)t * k + j];
+                if (ex < 0 || ex >= ne) throw rt_err("expert routing produced an invalid expert id");
+                assign[ex].emplace_back(t, w[(size_t)t * k + j]);
+            }
+        std::vector<int> rows;
+        std::vector<float> rw;
+        std::vector<int> off(ne + 1, 0);
+        for (int ex = 0; ex < ne; ex++) {
+            off[ex] = (int)rows.size();
+            for (auto &tw : assign[ex]) {
+                rows.push_back(tw.first);
+                rw.push_back(tw.second);
+            }
+        }
+        off[ne] = (int)rows.size();
+        RIE_HIP_CHECK(hipMemcpyAsync(d_moe_rows_, rows.data(), rows.size() * 4, hipMemcpyHostToDevice, st_));
+        RIE_HIP_CHECK(hipMemcpyAsync(d_moe_rw_, rw.data(), rw.size() * 4, hipMemcpyHostToDevice, st_));
+        RIE_HIP_CHECK(hipMemsetAsync(d_o_, 0, (size_t)n * E * 4, st_));
+        for (int ex = 0; ex < ne; ex++) {
+            const int m = off[ex + 1] - off[ex];
+            if (!m) continue;
+            launch_moe_gather(d_moe_xn_, d_moe_rows_ + off[ex], m, E, d_moe_xg_, st_);
+            expert_ffn(slice_rows(L.gate, (size_t)ex * ff, ff), slice_rows(L.up, (size_t)ex * ff, ff),
+                       slice_rows(L.down, (size_t)ex * E, E), d_moe_xg_, m, d_moe_yg_);
+            launch_moe_scatter_add(d_moe_yg_, d_moe_rows_ + off[ex], d_moe_rw_ + off[ex], m, E, d_o_, st_);
+        }
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));  // the host vectors above are read by the async copies
+    }
+    if (shared) {
+        expert_ffn(L.sh_gate, L.sh_up, L.sh_down, d_moe_xn_, n, d_moe_yg_);
+        launch_moe_shared_add(d_moe_yg_, L.sh_gate_inp, d_moe_xn_, n, E, d_o_, st_);
+    }
+    check_launch("moe");
+    mark("moe_combine");
 }
 
 void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_logits, float *logits, size_t logits_len) {

@@ -91,7 +91,8 @@ class HipBackend {
     void prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32);
     void matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0 = nullptr);
     void ffn_dense(const DevLayer &L, int n, float *out_resid, int epi);
-    void ffn_moe(const DevLayer &L, int n);
+    void ffn_moe(const DevLayer &L, int n);  // writes the block's output to d_o_
+    void expert_ffn(const DevWeight &g, const DevWeight &u, const DevWeight &dn, const float *x, int m, float *y);
     void head(int first, int m);
     void check_launch(const char *what);
     void decode_step_graph(size_t pos);
@@ -127,8 +128,9 @@ class HipBackend {
     ActQ8 act_h_;        // Q8_0 of the single-token FFN hidden
     size_t kmax_ = 0, ff_max_ = 0, part_floats_ = 0;
     // MoE scratch
-    float *d_router_ = nullptr, *d_moe_w_ = nullptr, *d_moe_h_ = nullptr, *d_moe_y_ = nullptr;
-    int *d_moe_sel_ = nullptr;
+    float *d_router_ = nullptr, *d_moe_w_ = nullptr, *d_moe_y_ = nullptr;
+    float *d_moe_xn_ = nullptr, *d_moe_xg_ = nullptr, *d_moe_yg_ = nullptr, *d_moe_rw_ = nullptr;
+    int *d_moe_sel_ = nullptr, *d_moe_rows_ = nullptr;
     float *d_kcap_ = nullptr;  // K after norm/RoPE when capturing
     int n_amax_part_ = 64;
 

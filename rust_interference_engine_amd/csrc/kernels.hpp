@@ -87,8 +87,21 @@ void launch_set_int(int *p, int v, hipStream_t st);
 void launch_softcap(float *x, size_t n, float cap, hipStream_t st);
 void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, const ActQ8 &act, hipStream_t st);
 // MoE routing: softmax over n_exp logits per token, top-k with index tie-break, renorm.
+// (sel, wgt) of each token are stored in ascending expert order.
 void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
                       hipStream_t st);
+// out[t] (= or +=) Σ_j w[t·k+j]·y[t·k+j] over the k routed experts (cpu.rs:502-513)
+void launch_moe_combine(const float *y, const float *w, int n_tok, int k, int E, float *out, int epi, hipStream_t st);
+void launch_moe_gather(const float *x, const int *rows, int n, int E, float *xg, hipStream_t st);
+void launch_moe_scatter_add(const float *yg, const int *rows, const float *w, int n, int E, float *out, hipStream_t st);
+void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *x, int n_tok, int E, float *out, hipStream_t st);
+// Routed experts of one token (stacked expert tensors, expert ids on the device):
+// out rows [j·slot_rows, (j+1)·slot_rows) = expert sel[j]'s rows · act (act row j
+// when act_per_slot); the GLU variant writes h [n_slots][ff].
+bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
+                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st);
+bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
+                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st);
 
 // ---- gemm.hip (prefill, int8 MFMA) ----
 bool gemm_supported(int ty, size_t K);

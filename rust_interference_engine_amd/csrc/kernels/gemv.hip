@@ -78,6 +78,11 @@ struct DecP {
     int glu;         // 0 none, 1 silu, 2 gelu
     ActQ8 hq;        // GLU: Q8_0 output of h when hq.qs != nullptr
     NormIn nin;      // nin.x != nullptr: the activation is RMSNorm(x)·w, quantized here
+    // routed experts: seg 0 (and seg 1 for GLU) hold the stacked expert matrices;
+    // rows [j·slot_rows, (j+1)·slot_rows) of the launch are rows of expert xsel[j]
+    const int *xsel;
+    int slot_rows;
+    int act_per_slot;  // slot j reads activation row j (the down projection of expert j's hidden)
 };
 
 // ---- per-type units --------------------------------------------------------
@@ -577,7 +582,15 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     const int seg_rows = p.seg[sg].rows;
     const int last = seg_rows - 1;
     const uint8_t *wbase = p.seg[sg].w;
+    const uint8_t *wbase2 = GLU ? p.seg[1].w : nullptr;
     const size_t rb = p.seg[sg].rb;
+    int slot = 0;
+    if (p.xsel) {  // a workgroup's rows lie in one slot (slot_rows is a multiple of the tile)
+        slot = row0 / p.slot_rows;
+        const size_t off = ((size_t)p.xsel[slot] - (size_t)slot) * (size_t)p.slot_rows * rb;
+        wbase += off;
+        if constexpr (GLU) wbase2 += ((size_t)p.xsel[slot] - (size_t)slot) * (size_t)p.slot_rows * p.seg[1].rb;
+    }
     Raw<TY> raw[NW][R][UPL];
     auto load_pass = [&](int base) {
 #pragma unroll
@@ -587,7 +600,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
 #pragma unroll
             for (int u = 0; u < UPL; u++) load_raw<TY>(row, uu[u], raw[0][k][u]);
             if constexpr (GLU) {
-                const uint8_t *row2 = p.seg[1].w + (size_t)r * p.seg[1].rb;
+                const uint8_t *row2 = wbase2 + (size_t)r * p.seg[1].rb;
 #pragma unroll
                 for (int u = 0; u < UPL; u++) load_raw<TY>(row2, uu[u], raw[1][k][u]);
             }
@@ -684,7 +697,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     if (!have_act) {
 #pragma unroll
         for (int k = 0; k < UPL; k++)
-            if (valid[k]) load_act<TY>(a[k], uu[k], p.act, p.actf, p.K);
+            if (valid[k]) load_act<TY>(a[k], uu[k], p.act, p.actf, p.K, p.act_per_slot ? slot : 0);
     }
     for (int base = base0; base < p.tr; base += GROUPS * R) {
         if (base != base0) load_pass(base);
@@ -801,6 +814,10 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         m = ov > 0 ? ov : std::max(1, std::min(4, p.total_rows / (pass * 1024)));
     }
     p.tr = pass * m;
+    if (p.xsel && p.slot_rows % p.tr) {  // a workgroup must not straddle two experts
+        p.tr = pass;
+        if (p.slot_rows % p.tr || (p.glu && p.hq.qs && p.tr % 32)) return false;
+    }
     const size_t lds = ((size_t)(p.glu ? 2 : 1) * p.tr * (lpr + DEC_PAD) + p.tr) * sizeof(float);
     if (lds > 64 * 1024) return false;
     int blocks = 0;
@@ -959,6 +976,45 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
         i = j;
     }
     return true;
+}
+
+bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
+                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st) {
+    if (!gemv_supported(stacked.ty, (size_t)K) || stacked.cols != (size_t)K || !stacked.data || !out || !sel || n_slots < 1 ||
+        slot_rows < 1 || stacked.rows % (size_t)slot_rows || !operands_ok(stacked.ty, act, act_f32))
+        return false;
+    DecP d{};
+    d.seg[0] = SegP{stacked.data, stacked.rb(), slot_rows * n_slots, out, slot_rows * n_slots, EPI_STORE};
+    d.nseg = 1;
+    d.total_rows = slot_rows * n_slots;
+    d.K = K;
+    d.act = act;
+    d.actf = act_f32;
+    d.xsel = sel;
+    d.slot_rows = slot_rows;
+    d.act_per_slot = act_per_slot;
+    return dispatch_dec(stacked.ty, d, st);
+}
+
+bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
+                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st) {
+    if (gate.ty != up.ty || !gemv_supported(gate.ty, (size_t)K) || gate.cols != (size_t)K || up.cols != (size_t)K ||
+        gate.rows != up.rows || gate.rows % (size_t)ff || !gate.data || !up.data || !h || !sel || n_slots < 1 ||
+        !operands_ok(gate.ty, act, act_f32))
+        return false;
+    DecP d{};
+    d.seg[0] = SegP{gate.data, gate.rb(), ff * n_slots, h, ff * n_slots, EPI_STORE};
+    d.seg[1] = SegP{up.data, up.rb(), ff * n_slots, h, ff * n_slots, EPI_STORE};
+    d.nseg = 2;
+    d.total_rows = ff * n_slots;
+    d.K = K;
+    d.act = act;
+    d.actf = act_f32;
+    d.glu = gelu ? 2 : 1;
+    if (hq) d.hq = *hq;
+    d.xsel = sel;
+    d.slot_rows = ff;
+    return dispatch_dec(gate.ty, d, st);
 }
 
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,

@@ -133,11 +133,80 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
             norm = 0.0f;
             for (int j = 0; j < k; j++) norm += cval[j];
         }
+        // store in ascending expert order: the CPU path adds the experts' outputs
+        // in that order (cpu.rs:502-513), and so does launch_moe_combine
         for (int j = 0; j < k; j++) {
-            sel[(size_t)t * k + j] = chosen[j];
-            wgt[(size_t)t * k + j] = unit_weights ? 1.0f : cval[j] / norm;
+            int lo = -1;
+            for (int q = 0; q < k; q++)
+                if (chosen[q] >= 0 && (lo < 0 || chosen[q] < chosen[lo])) lo = q;
+            sel[(size_t)t * k + j] = chosen[lo];
+            wgt[(size_t)t * k + j] = unit_weights ? 1.0f : cval[lo] / norm;
+            chosen[lo] = -1;
         }
     }
+}
+
+// out[t] (= or +=) Σ_j w[t][j]·y[t·k + j], j in ascending expert order, starting from 0
+__global__ void moe_combine_kernel(const float *__restrict__ y, const float *__restrict__ w, int k, int E, float *__restrict__ out,
+                                   int epi) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= E) return;
+    float o = 0.0f;
+    for (int j = 0; j < k; j++) o += w[(size_t)t * k + j] * y[((size_t)t * k + j) * E + i];
+    if (epi == EPI_ADD) out[(size_t)t * E + i] += o;
+    else out[(size_t)t * E + i] = o;
+}
+
+void launch_moe_combine(const float *y, const float *w, int n_tok, int k, int E, float *out, int epi, hipStream_t st) {
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((E + 255) / 256, n_tok), dim3(256), 0, st, y, w, k, E, out, epi);
+}
+
+// xg[i] = x[rows[i]]  (rows of E floats)
+__global__ void moe_gather_kernel(const float *__restrict__ x, const int *__restrict__ rows, int E, float *__restrict__ xg) {
+    const int r = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i < E) xg[(size_t)r * E + i] = x[(size_t)rows[r] * E + i];
+}
+
+void launch_moe_gather(const float *x, const int *rows, int n, int E, float *xg, hipStream_t st) {
+    hipLaunchKernelGGL(moe_gather_kernel, dim3((E + 255) / 256, n), dim3(256), 0, st, x, rows, E, xg);
+}
+
+// out[rows[i]] += w[i]·yg[i]; one expert's rows are distinct tokens, so no two
+// threads of a launch touch the same element
+__global__ void moe_scatter_add_kernel(const float *__restrict__ yg, const int *__restrict__ rows, const float *__restrict__ w, int E,
+                                       float *__restrict__ out) {
+    const int r = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i < E) out[(size_t)rows[r] * E + i] += w[r] * yg[(size_t)r * E + i];
+}
+
+void launch_moe_scatter_add(const float *yg, const int *rows, const float *w, int n, int E, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(moe_scatter_add_kernel, dim3((E + 255) / 256, n), dim3(256), 0, st, yg, rows, w, E, out);
+}
+
+// out[t] += sigmoid(g·x[t])·ys[t] (shared expert gate, cpu.rs:516-522); g may be null (scale 1)
+__global__ __launch_bounds__(256) void moe_shared_add_kernel(const float *__restrict__ ys, const float *__restrict__ g,
+                                                             const float *__restrict__ x, int E, float *__restrict__ out) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    __shared__ float red[4];
+    __shared__ float s_scale;
+    if (g) {
+        float s = 0.0f;
+        for (int i = tid; i < E; i += 256) s = fmaf(g[i], x[(size_t)t * E + i], s);
+        s = wave_sum(s, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = s;
+        __syncthreads();
+        if (tid == 0) s_scale = 1.0f / (1.0f + expf(-((red[0] + red[1]) + (red[2] + red[3]))));
+        __syncthreads();
+    } else if (tid == 0) {
+        s_scale = 1.0f;
+    }
+    __syncthreads();
+    const float sc = s_scale;
+    for (int i = tid; i < E; i += 256) out[(size_t)t * E + i] += sc * ys[(size_t)t * E + i];
+}
+
+void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *x, int n_tok, int E, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(moe_shared_add_kernel, dim3(n_tok), dim3(256), 0, st, ys, gate_inp, x, E, out);
 }
 
 void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,

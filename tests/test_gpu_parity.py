@@ -294,6 +294,34 @@ def test_prompt_batches_through_gemm_match_oracle(oracle, cuda, arch, ty):
             assert err < 0.03, f"{arch} {ty}: token {pos + t}: {err}"
 
 
+MOE_CASES = [  # (arch, weight type, tolerance, mutate): routed experts, shared expert + sigmoid gate, Q8_0 and Q8_K experts
+    ("qwen3moe", F16, 3e-3, None), ("qwen2moe", F16, 3e-3, None), ("qwen3moe", Q4_K, 0.03, None),
+    ("qwen3moe", Q4_0, 0.03, None), ("llama", Q8_0, 0.03, "mixtral"),
+]
+
+
+@pytest.mark.parametrize("arch,ty,tol,mut", MOE_CASES)
+def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
+    """moe_ffn (cpu.rs:469-524): prompt batches (experts over gathered tokens)
+    and single-token decode (routing and expert choice on the device, graph
+    replay) against the oracle."""
+    from naive_model import max_rel_err
+
+    def mixtral(s):
+        s.n_expert, s.n_expert_used, s.n_ff_exp = 4, 2, 512
+    spec, g, o = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16, mutate=mixtral if mut == "mixtral" else None)
+    nv = spec.n_vocab
+    toks = [(i * 41 + 7) % nv for i in range(20)]
+    lg = g.forward(toks[:16], 0, True)
+    lo = o.forward(toks[:16], 0, True)
+    for t in range(16):
+        err = max_rel_err(lg[t * nv:(t + 1) * nv], lo[t * nv:(t + 1) * nv])
+        assert err < tol, f"{arch} {ty}: batched token {t}: {err}"
+    for t in range(16, 20):
+        err = max_rel_err(g.forward([toks[t]], t), o.forward([toks[t]], t))
+        assert err < tol, f"{arch} {ty}: decode token {t}: {err}"
+
+
 ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32, query groups 1..8
     (32, 4, 4), (128, 8, 2), (256, 8, 1), (64, 8, 1), (128, 6, 2),
 ]
