@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <type_traits>
 
 namespace rie {
 
@@ -41,20 +42,70 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return b;
 }
 
-__device__ __forceinline__ float wave_sum(float v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Value held by lane (this lane xor OFF): one ds_swizzle (bitmask mode, within a
+// 32-lane half) for OFF < 32, one ds_bpermute for OFF = 32; no per-call lane-id
+// arithmetic.  Call with the source lanes active.
+template <int OFF>
+__device__ __forceinline__ int xor_i(int v) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane offset");
+    if constexpr (OFF == 32) return __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), v);
+    else return __builtin_amdgcn_ds_swizzle(v, 0x1F | (OFF << 10));
+}
+template <int OFF>
+__device__ __forceinline__ float xor_f(float v) { return __int_as_float(xor_i<OFF>(__float_as_int(v))); }
+
+// f(std::integral_constant<int, O>) for O = FROM, FROM/2, …, TO, or (xor_up) for
+// O = FROM, 2·FROM, …, TO: lane-offset loops whose offsets are template arguments.
+template <int FROM, int TO, class F>
+__device__ __forceinline__ void xor_down(F &&f) {
+    if constexpr (FROM >= TO && FROM >= 1) {
+        f(std::integral_constant<int, FROM>{});
+        xor_down<FROM / 2, TO>(f);
+    }
+}
+template <int FROM, int TO, class F>
+__device__ __forceinline__ void xor_up(F &&f) {
+    if constexpr (FROM <= TO) {
+        f(std::integral_constant<int, FROM>{});
+        xor_up<FROM * 2, TO>(f);
+    }
+}
+
+// butterfly reductions over aligned groups of W lanes (offsets W/2 … 1)
+template <int W>
+__device__ __forceinline__ float xsum_f(float v) {
+    xor_down<W / 2, 1>([&](auto o) { v += xor_f<decltype(o)::value>(v); });
     return v;
+}
+template <int W>
+__device__ __forceinline__ int xsum_i(int v) {
+    xor_down<W / 2, 1>([&](auto o) { v += xor_i<decltype(o)::value>(v); });
+    return v;
+}
+template <int W>
+__device__ __forceinline__ float xmax_f(float v) {
+    xor_down<W / 2, 1>([&](auto o) { v = fmaxf(v, xor_f<decltype(o)::value>(v)); });
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v, int width) {
+    return width >= 64 ? xsum_f<64>(v) : width >= 32 ? xsum_f<32>(v) : width >= 16 ? xsum_f<16>(v) : width >= 8 ? xsum_f<8>(v)
+         : width >= 4 ? xsum_f<4>(v) : width >= 2 ? xsum_f<2>(v) : v;
 }
 
 __device__ __forceinline__ int wave_sum_i(int v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return width >= 64 ? xsum_i<64>(v) : width >= 32 ? xsum_i<32>(v) : width >= 16 ? xsum_i<16>(v) : width >= 8 ? xsum_i<8>(v)
+         : width >= 4 ? xsum_i<4>(v) : width >= 2 ? xsum_i<2>(v) : v;
 }
 
 __device__ __forceinline__ float wave_max(float v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    return width >= 64 ? xmax_f<64>(v) : width >= 32 ? xmax_f<32>(v) : width >= 16 ? xmax_f<16>(v) : width >= 8 ? xmax_f<8>(v)
+         : width >= 4 ? xmax_f<4>(v) : width >= 2 ? xmax_f<2>(v) : v;
 }
+
+// 2^x by the hardware exponential (v_exp_f32): exp2(-inf) = 0
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr float LOG2E_F = 1.44269504088896340736f;
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
@@ -107,7 +158,7 @@ __device__ __forceinline__ float group_sum(float v) {
         v += dpp_f<DPP_ROW_ROR4>(v);
         v += dpp_f<DPP_ROW_ROR8>(v);
     }
-    if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W == 32) v += xor_f<16>(v);
     return v;
 }
 // exact integer sum over the 4 lanes of a quad
@@ -115,6 +166,26 @@ __device__ __forceinline__ int quad_sum_i(int v) {
     v += dpp_i<DPP_QUAD_XOR1>(v);
     v += dpp_i<DPP_QUAD_XOR2>(v);
     return v;
+}
+
+// Agent-coherent accesses: a relaxed agent-scope store writes through to the
+// device coherence point and a relaxed agent-scope load reads from it, so data
+// passed between workgroups on different XCDs needs no L2 write-back or
+// invalidate.
+__device__ __forceinline__ void st_coh(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_coh(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Waits until this wave's outstanding vector memory operations, stores included,
+// have completed (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima in
+// the gfx9 encoding).  After st_coh stores this makes them visible device-wide.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Orders one wavefront's LDS accesses across its lanes (a wave's LDS operations
+// execute in issue order; the fences stop the compiler from moving accesses
+// across this point).  For code run by a single wave of a larger workgroup.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 }  // namespace rie

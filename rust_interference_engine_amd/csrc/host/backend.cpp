@@ -216,6 +216,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
     part_floats_ = (size_t)std::max<size_t>(32 * mb, ATT_MAX_SPLIT) * c.n_head * (hd + 2);
     d_part_ = dalloc<float>(allocs_, part_floats_);
+    d_attn_cnt_ = dalloc<int>(allocs_, c.n_head_kv * ATT_CNT_STRIDE);
     d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
     if (c.n_expert) {
@@ -404,18 +405,7 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
             cap_[5][il].resize((size_t)n * kvd);
             RIE_HIP_CHECK(hipMemcpy(cap_[5][il].data(), d_v_, (size_t)n * kvd * 4, hipMemcpyDeviceToHost));
         }
-        launch_head_prep(hp, st_);
-        check_launch("head_prep");
-        mark("head_prep_kv_append");
-        if (capture_ && !in_capture_) {
-            RIE_HIP_CHECK(hipStreamSynchronize(st_));
-            cap_[3].resize(c.n_layer);
-            cap_[3][il].resize((size_t)n * qd);
-            RIE_HIP_CHECK(hipMemcpy(cap_[3][il].data(), d_q_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
-            cap_[4].resize(c.n_layer);
-            cap_[4][il].resize((size_t)n * kvd);
-            RIE_HIP_CHECK(hipMemcpy(cap_[4][il].data(), d_kcap_, (size_t)n * kvd * 4, hipMemcpyDeviceToHost));
-        }
+        const int wo_fmt = act_format(L.wo.ty);
         AttnArgs aa{};
         aa.q = d_q_;
         aa.k_cache = L.k_cache; aa.v_cache = L.v_cache; aa.k_scale = L.k_scale; aa.v_scale = L.v_scale;
@@ -425,16 +415,36 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         aa.part = d_part_;
         aa.n_split = n_split;
         aa.att = d_att_;
-        const int wo_fmt = act_format(L.wo.ty);
         aa.att_fmt = wo_fmt == ACT_Q8_0 ? ACT_Q8_0 : -1;
         aa.att_q = act0_;
         aa.d_pos0 = d_pos0;
         aa.turbo_signs = d_signs_;
-        launch_attention(aa, st_);
+        aa.counters = d_attn_cnt_;
+        // single token: prep, append, attention and range merge in one launch
+        const bool fused_attn = n == 1 && attention_fused_ok(aa);
+        if (!fused_attn) {
+            launch_head_prep(hp, st_);
+            check_launch("head_prep");
+            mark("head_prep_kv_append");
+            if (capture_ && !in_capture_) {  // the prepared query exists in memory only on this path
+                RIE_HIP_CHECK(hipStreamSynchronize(st_));
+                cap_[3].resize(c.n_layer);
+                cap_[3][il].resize((size_t)n * qd);
+                RIE_HIP_CHECK(hipMemcpy(cap_[3][il].data(), d_q_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
+            }
+        }
+        if (fused_attn) {
+            if (!launch_attention_fused(aa, hp, st_)) throw rt_err("fused attention launch rejected");
+        } else {
+            launch_attention(aa, st_);
+        }
         check_launch("attention");
         mark("attention");
         if (capture_ && !in_capture_) {
             RIE_HIP_CHECK(hipStreamSynchronize(st_));
+            cap_[4].resize(c.n_layer);
+            cap_[4][il].resize((size_t)n * kvd);
+            RIE_HIP_CHECK(hipMemcpy(cap_[4][il].data(), d_kcap_, (size_t)n * kvd * 4, hipMemcpyDeviceToHost));
             cap_[2].resize(c.n_layer);
             cap_[2][il].resize((size_t)n * qd);
             RIE_HIP_CHECK(hipMemcpy(cap_[2][il].data(), d_att_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));

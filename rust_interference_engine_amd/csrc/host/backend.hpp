@@ -124,6 +124,7 @@ class HipBackend {
     float *d_x_ = nullptr, *d_xn_ = nullptr, *d_q_ = nullptr, *d_k_ = nullptr, *d_v_ = nullptr, *d_att_ = nullptr, *d_h_ = nullptr,
           *d_o_ = nullptr, *d_logits_ = nullptr, *d_part_ = nullptr, *d_amax_val_ = nullptr, *d_gemm_ws_ = nullptr;
     int *d_amax_idx_ = nullptr;
+    int *d_attn_cnt_ = nullptr;  // per-KV-head arrival counters of the fused single-token attention
     ActQ8 act0_, actk_;  // Q8_0 and Q8_K batches
     ActQ8 act_h_;        // Q8_0 of the single-token FFN hidden
     size_t kmax_ = 0, ff_max_ = 0, part_floats_ = 0;

@@ -73,8 +73,14 @@ struct AttnArgs {
     int att_fmt;
     const int *d_pos0;
     const float *turbo_signs;
+    int *counters;               // fused single-token path: [n_kv · ATT_CNT_STRIDE] zeroed ints, left zeroed
 };
+constexpr int ATT_CNT_STRIDE = 32;  // ints between the per-KV-head arrival counters
 void launch_attention(const AttnArgs &a, hipStream_t st);
+// Single token: Q/K prep, KV append, attention and the range merge in one launch
+// (hp describes the raw Q/K/V rows; hp.q is only read).  False when not applicable.
+bool attention_fused_ok(const AttnArgs &a);
+bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st);
 // number of context ranges (n_split) for a launch whose longest query sees max_len positions
 constexpr int ATT_MAX_SPLIT = 256;
 int attention_splits(int n_tok, int n_kv, int max_len);

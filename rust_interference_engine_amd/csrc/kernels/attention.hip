@@ -28,41 +28,60 @@ namespace rie {
 
 __constant__ int8_t KV_LEVELS_I8[16] = {-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126};
 
-__device__ __forceinline__ int turbo_block(int d) {
+__host__ __device__ constexpr int turbo_block(int d) {
     int b = 1;
     while (d % (b * 2) == 0 && b < 256) b *= 2;
     return b;
 }
 
-// one wavefront per (head vector, token); x lives in LDS during the transform
-__global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
-    const int t = blockIdx.y;
-    const int hh = blockIdx.x;
-    const int lane = threadIdx.x;
-    const int hd = a.hd;
-    const int pos0 = a.d_pos0 ? *a.d_pos0 : a.pos0;
-    const int pos = pos0 + t;
+// One wavefront prepares one head vector of token t at position pos: bias,
+// per-head RMSNorm (q, k), RoPE (q, k); a query is scaled and written to q_dst,
+// a key/value row is appended to the cache (and K to k_out when set).  With
+// mirror set, the encoded row (and its Turbo4 scales) is also written there as
+// one cache row of a one-row cache: [row bytes | f16 scales at KV_MIRROR_SC].
+// xs, ys: this wave's LDS scratch, 256 floats each; s_inv: 8 floats.
+// HD > 0: the head size as a compile-time constant (HD = a.hd).
+constexpr int KV_MIRROR_SC = 512;  // byte offset of the scales in a mirror row
+template <int HD>
+__device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, int pos, float *q_dst, float *xs, float *ys,
+                               float *s_inv, uint8_t *mirror = nullptr) {
+    const int lane = threadIdx.x & 63;
+    const int hd = HD > 0 ? HD : a.hd;
     const int qd = a.n_head * hd, kvd = a.n_kv * hd;
-    __shared__ float xs[256];
-    __shared__ float ys[256];
-    int kind;  // 0 q, 1 k, 2 v
-    int h;
     const float *src;
     const float *bias;
     const float *nw;
-    if (hh < a.n_head) {
-        kind = 0; h = hh; src = a.q + (size_t)t * qd + h * hd; bias = a.bq; nw = a.q_norm;
-    } else if (hh < a.n_head + a.n_kv) {
-        kind = 1; h = hh - a.n_head; src = a.k + (size_t)t * kvd + h * hd; bias = a.bk; nw = a.k_norm;
+    if (kind == 0) {
+        src = a.q + (size_t)t * qd + h * hd; bias = a.bq; nw = a.q_norm;
+    } else if (kind == 1) {
+        src = a.k + (size_t)t * kvd + h * hd; bias = a.bk; nw = a.k_norm;
     } else {
-        kind = 2; h = hh - a.n_head - a.n_kv; src = a.v + (size_t)t * kvd + h * hd; bias = a.bv; nw = nullptr;
+        src = a.v + (size_t)t * kvd + h * hd; bias = a.bv; nw = nullptr;
     }
-    for (int e = lane; e < hd; e += 64) {
-        float x = src[e];
-        if (bias) x += bias[h * hd + e];
-        xs[e] = x;
+    // this lane's elements e = lane + 64k and their RoPE table entries, loads issued together
+    const int half = a.rope_dim / 2;
+    const float *ct = a.cos_t + (size_t)pos * half;
+    const float *st = a.sin_t + (size_t)pos * half;
+    float xr[4], cr[4], sr[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        xr[k] = cr[k] = sr[k] = 0.0f;
+        if (e < hd) {
+            xr[k] = src[e];
+            if (kind < 2 && e < a.rope_dim) {
+                const int i = a.neox ? (e < half ? e : e - half) : (e >> 1);
+                cr[k] = ct[i];
+                sr[k] = st[i];
+            }
+        }
     }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        if (e < hd) xs[e] = bias ? xr[k] + bias[h * hd + e] : xr[k];
+    }
+    wave_sync();
     if (kind < 2) {
         if (nw) {  // ops.rs:17-24: x *= scale·w
             float ss = 0.0f;
@@ -70,34 +89,33 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
             ss = wave_sum(ss, 64);
             const float scale = 1.0f / sqrtf(ss / (float)hd + a.eps);
             for (int e = lane; e < hd; e += 64) xs[e] = xs[e] * (scale * nw[e]);
-            __syncthreads();
+            wave_sync();
         }
         // RoPE, ops.rs:93-108, with the host-computed cos/sin table row of this position
-        const int half = a.rope_dim / 2;
-        const float *ct = a.cos_t + (size_t)pos * half;
-        const float *st = a.sin_t + (size_t)pos * half;
-        for (int e = lane; e < hd; e += 64) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = lane + 64 * k;
+            if (e >= hd) break;
             float y = xs[e];
             if (e < a.rope_dim) {
                 if (a.neox) {
                     const int i = e < half ? e : e - half;
                     const float x0 = xs[i], x1 = xs[i + half];
-                    y = e < half ? x0 * ct[i] - x1 * st[i] : x0 * st[i] + x1 * ct[i];
+                    y = e < half ? x0 * cr[k] - x1 * sr[k] : x0 * sr[k] + x1 * cr[k];
                 } else {
                     const int i = e >> 1;
                     const float x0 = xs[2 * i], x1 = xs[2 * i + 1];
-                    y = (e & 1) == 0 ? x0 * ct[i] - x1 * st[i] : x0 * st[i] + x1 * ct[i];
+                    y = (e & 1) == 0 ? x0 * cr[k] - x1 * sr[k] : x0 * sr[k] + x1 * cr[k];
                 }
             }
             ys[e] = y;
         }
-        __syncthreads();
+        wave_sync();
         for (int e = lane; e < hd; e += 64) xs[e] = ys[e];
-        __syncthreads();
+        wave_sync();
     }
     if (kind == 0) {
-        float *dst = a.q + (size_t)t * qd + h * hd;
-        for (int e = lane; e < hd; e += 64) dst[e] = xs[e] * a.attn_scale;
+        for (int e = lane; e < hd; e += 64) q_dst[e] = xs[e] * a.attn_scale;
         return;
     }
     if (a.k_out && kind == 1)
@@ -107,7 +125,11 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
     uint8_t *cache = kind == 1 ? a.k_cache : a.v_cache;
     if (a.kv_type == 0) {
         uint16_t *dst = (uint16_t *)cache + row * hd;
-        for (int e = lane; e < hd; e += 64) dst[e] = f2h(xs[e]);
+        for (int e = lane; e < hd; e += 64) {
+            const uint16_t hb = f2h(xs[e]);
+            dst[e] = hb;
+            if (mirror) ((uint16_t *)mirror)[e] = hb;
+        }
     } else if (a.kv_type == 1) {
         // store_q8_0 (cpu.rs:637-647): round half away from zero, f16 scale
         uint8_t *dst = cache + row * (size_t)(hd / 32 * 34);
@@ -115,26 +137,30 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
             const int e = e0 + lane;
             const float x = e < hd ? xs[e] : 0.0f;
             float amax = fabsf(x);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+            amax = xmax_f<32>(amax);
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             int q = (int)roundf(x * id);
             q = q < -127 ? -127 : (q > 127 ? 127 : q);
             if (e < hd) {
-                uint8_t *blk = dst + (e >> 5) * 34;
-                blk[2 + (e & 31)] = (uint8_t)(int8_t)q;
+                const int off = (e >> 5) * 34;
+                dst[off + 2 + (e & 31)] = (uint8_t)(int8_t)q;
+                if (mirror) mirror[off + 2 + (e & 31)] = (uint8_t)(int8_t)q;
                 if ((e & 31) == 0) {
                     const uint16_t hb = f2h(d);
-                    blk[0] = (uint8_t)hb;
-                    blk[1] = (uint8_t)(hb >> 8);
+                    dst[off] = (uint8_t)hb;
+                    dst[off + 1] = (uint8_t)(hb >> 8);
+                    if (mirror) {
+                        mirror[off] = (uint8_t)hb;
+                        mirror[off + 1] = (uint8_t)(hb >> 8);
+                    }
                 }
             }
         }
     } else {
         // TurboQuant-4 (turbo.rs:140-171): signs, block FWHT, RMS codes, LS scale
         for (int e = lane; e < hd; e += 64) xs[e] *= a.turbo_signs[e];
-        __syncthreads();
+        wave_sync();
         const int b = turbo_block(hd);
         for (int hstep = 1; hstep < b; hstep *= 2) {
             for (int k = lane; k < hd / 2; k += 64) {
@@ -144,18 +170,17 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
                 xs[j] = x0 + x1;
                 xs[j + hstep] = x0 - x1;
             }
-            __syncthreads();
+            wave_sync();
         }
         const float s = 1.0f / sqrtf((float)b);
         for (int e = lane; e < hd; e += 64) xs[e] *= s;
-        __syncthreads();
+        wave_sync();
         float c[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) c[i] = (float)KV_LEVELS_I8[i] / 46.0f;
         uint8_t *codes = cache + row * (size_t)(hd / 2);
         uint16_t *scales = (kind == 1 ? a.k_scale : a.v_scale) + row * (size_t)(hd / b);
-        __shared__ float s_inv[8];
-        __shared__ uint8_t qv[256];
+        uint8_t *qv = (uint8_t *)ys;  // 256 code bytes
         const int nbk = hd / b;
         if (lane < nbk) {  // sequential f32 sums, the reference's order
             float ss = 0.0f;
@@ -163,7 +188,7 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
             const float rms = sqrtf(ss / (float)b);
             s_inv[lane] = rms > 0.0f ? 1.0f / rms : 0.0f;
         }
-        __syncthreads();
+        wave_sync();
         for (int e = lane; e < hd; e += 64) {
             const float v = xs[e] * s_inv[e / b];
             uint8_t q = 0;
@@ -171,10 +196,11 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
             for (int k = 0; k < 15; k++) q += (uint8_t)(v > 0.5f * (c[k] + c[k + 1]));
             qv[e] = q;
         }
-        __syncthreads();
+        wave_sync();
         for (int i = lane; i < hd / 2; i += 64) {  // byte i holds values g (low) and g+16 (high) of its 32-chunk
             const int g = (i / 16) * 32 + (i % 16);
             codes[i] = (uint8_t)(qv[g] | (qv[g + 16] << 4));
+            if (mirror) mirror[i] = (uint8_t)(qv[g] | (qv[g + 16] << 4));
         }
         if (lane < nbk) {
             float num = 0.0f, den = 0.0f;
@@ -184,8 +210,28 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
                 den += cq * cq;
             }
             scales[lane] = f2h(den > 0.0f ? num / den : 0.0f);
+            if (mirror) ((uint16_t *)(mirror + KV_MIRROR_SC))[lane] = f2h(den > 0.0f ? num / den : 0.0f);
         }
     }
+}
+
+// one wavefront per (head vector, token); the query is rewritten in place
+__global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
+    const int t = blockIdx.y;
+    const int hh = blockIdx.x;
+    const int pos0 = a.d_pos0 ? *a.d_pos0 : a.pos0;
+    __shared__ float xs[256];
+    __shared__ float ys[256];
+    __shared__ float s_inv[8];
+    int kind, h;
+    if (hh < a.n_head) {
+        kind = 0; h = hh;
+    } else if (hh < a.n_head + a.n_kv) {
+        kind = 1; h = hh - a.n_head;
+    } else {
+        kind = 2; h = hh - a.n_head - a.n_kv;
+    }
+    prep_head_wave<0>(a, kind, h, t, pos0 + t, a.q + (size_t)t * a.n_head * a.hd + h * a.hd, xs, ys, s_inv);
 }
 
 void launch_head_prep(const HeadPrepArgs &a, hipStream_t st) {
@@ -270,6 +316,122 @@ __device__ __forceinline__ void chunk_values(const KvChunk<KVT> &c, int d0, floa
     }
 }
 
+// The last workgroup of KV head g to finish merges the n_split ranges of the
+// group's query heads (flash-decoding combine), undoes the TurboQuant rotation
+// and writes att (f32, and Q8_0 when att_fmt asks).  256 threads.
+// Scores of ATT_NP positions × MG query heads: each lane's partial dot over its 8
+// dims, summed over the SUB lanes of the position (every lane of the group gets
+// the sum).  Q8_0 / Turbo4 caches: per-block integer dots (cpu.rs: int32 block
+// sums) over the 4 lanes of a block, scaled by d_k·d_q.
+template <int KVT, int SUB, int MG>
+__device__ __forceinline__ void tile_scores(const KvChunk<KVT> (&kc)[ATT_NP], const float (&qf)[MG][8], const uint32_t (&qq)[MG][2],
+                                            const float (&qdd)[MG], int c, bool cact, int d0, float (&sc)[ATT_NP][MG]) {
+#pragma unroll
+    for (int n = 0; n < ATT_NP; n++) {
+        float kf[8];
+        if constexpr (KVT == 0) chunk_values<0>(kc[n], d0, kf);
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            float part = 0.0f;
+            if constexpr (KVT == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) part = fmaf(kf[i], qf[j][i], part);
+            } else {
+                uint32_t kw[2];
+                if constexpr (KVT == 1) {
+                    kw[0] = kc[n].raw.x;
+                    kw[1] = kc[n].raw.y;
+                } else {
+                    turbo_levels8(kc[n], (d0 % 32) >= 16, kw);
+                }
+                const int isum = quad_sum_i(sdot4(kw[1], qq[j][1], sdot4(kw[0], qq[j][0], 0)));
+                const float ks = KVT == 1 ? h2f(kc[n].sc) : h2f(kc[n].sc) * (1.0f / 46.0f);
+                part = (c & 3) == 0 ? (KVT == 1 ? ks * qdd[j] : qdd[j] * ks) * (float)isum : 0.0f;
+            }
+            if (!cact) part = 0.0f;
+            sc[n][j] = group_sum<SUB>(part);
+        }
+    }
+}
+
+// The group's query heads (in qs_f, f32) → Turbo4 rotation and Q8_0 codes
+// (cpu.rs:585-598) for quantized caches, then this lane's registers.  256 threads.
+template <int KVT, int MG>
+__device__ __forceinline__ void query_registers(const AttnArgs &a, int G, int hd, int tb, int d0, float *qs_f, int8_t *qs_i, float *qs_d,
+                                                float (&qf)[MG][8], uint32_t (&qq)[MG][2], float (&qdd)[MG]) {
+    const int tid = threadIdx.x;
+    if constexpr (KVT != 0) {
+        if constexpr (KVT == 2) {
+            for (int j = 0; j < G; j++) {
+                float *x = qs_f + j * hd;
+                for (int e = tid; e < hd; e += 256) x[e] *= a.turbo_signs[e];
+                __syncthreads();
+                for (int hstep = 1; hstep < tb; hstep *= 2) {
+                    for (int k = tid; k < hd / 2; k += 256) {
+                        const int blk = k / (tb / 2), kk = k % (tb / 2);
+                        const int jj = blk * tb + (kk / hstep) * 2 * hstep + (kk % hstep);
+                        const float x0 = x[jj], x1 = x[jj + hstep];
+                        x[jj] = x0 + x1;
+                        x[jj + hstep] = x0 - x1;
+                    }
+                    __syncthreads();
+                }
+                const float sq = 1.0f / sqrtf((float)tb);
+                for (int e = tid; e < hd; e += 256) x[e] *= sq;
+                __syncthreads();
+            }
+        }
+        // RNE Q8_0 quantization of each 32-block, half a wave per block
+        const int hw = tid >> 5, j = tid & 31;
+        for (int bi = hw; bi < G * hd / 32; bi += 8) {
+            const float y = qs_f[bi * 32 + j];
+            float amax = fabsf(y);
+            amax = xmax_f<32>(amax);
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            int q = (int)rintf(y * id);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            qs_i[bi * 32 + j] = (int8_t)q;
+            if (j == 0) qs_d[bi] = d;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < MG; j++) {
+        const int jj = j < G ? j : 0;
+        if constexpr (KVT == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) qf[j][i] = qs_f[jj * hd + d0 + i];
+            qq[j][0] = qq[j][1] = 0;
+            qdd[j] = 0.0f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) qf[j][i] = 0.0f;
+            qq[j][0] = *(const uint32_t *)(qs_i + jj * hd + d0);
+            qq[j][1] = *(const uint32_t *)(qs_i + jj * hd + d0 + 4);
+            qdd[j] = qs_d[(jj * hd) / 32 + d0 / 32];
+        }
+    }
+}
+
+// K and V chunks of ATT_NP positions tile + pi + PP·n (rows past r1 repeat row r0)
+template <int KVT, int PP>
+__device__ __forceinline__ void load_tile(const AttnArgs &a, size_t kv_row0, int tile, int pi, int r0, int r1, int hd, int d0, int tb,
+                                          KvChunk<KVT> (&kc)[ATT_NP], KvChunk<KVT> (&vc)[ATT_NP], bool (&ok)[ATT_NP]) {
+#pragma unroll
+    for (int n = 0; n < ATT_NP; n++) {
+        const int pos = tile + pi + PP * n;
+        ok[n] = pos < r1;
+        const int q = ok[n] ? pos : r0;
+        const size_t row = kv_row0 + (size_t)(q < a.slots ? q : q % a.slots);
+        load_chunk<KVT>(a.k_cache, a.k_scale, row, hd, d0, tb, kc[n]);
+        load_chunk<KVT>(a.v_cache, a.v_scale, row, hd, d0, tb, vc[n]);
+    }
+}
+
+// Prompt tokens: one workgroup per (range, kv head, token); per tile of positions
+// the scores go through LDS, the online softmax runs one wavefront per query head,
+// and the V accumulation is per lane; the position slots are summed at the end.
 template <int KVT, int SUB, int MG>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     constexpr int PP = 256 / SUB;  // position slots per pass
@@ -297,114 +459,35 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     __shared__ float sc[MG][TP];       // scores → probabilities of one tile
     __shared__ float m_run[MG], l_run[MG], alpha[MG];
 
+    const size_t kv_row0 = (size_t)g * a.slots;
+    KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
+    bool ok[ATT_NP];
+    if (r0 < r1) load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // overlaps the query load
     for (int i = tid; i < G * hd; i += 256) qs_f[i] = a.q[(size_t)t * qd + (size_t)g * G * hd + i];
     if (tid < MG) {
         m_run[tid] = -INFINITY;
         l_run[tid] = 0.0f;
     }
     __syncthreads();
-    if constexpr (KVT != 0) {
-        // the query is rotated (Turbo4) and quantized to Q8_0 once (cpu.rs:585-598)
-        if constexpr (KVT == 2) {
-            for (int j = 0; j < G; j++) {
-                float *x = qs_f + j * hd;
-                for (int e = tid; e < hd; e += 256) x[e] *= a.turbo_signs[e];
-                __syncthreads();
-                for (int hstep = 1; hstep < tb; hstep *= 2) {
-                    for (int k = tid; k < hd / 2; k += 256) {
-                        const int blk = k / (tb / 2), kk = k % (tb / 2);
-                        const int jj = blk * tb + (kk / hstep) * 2 * hstep + (kk % hstep);
-                        const float x0 = x[jj], x1 = x[jj + hstep];
-                        x[jj] = x0 + x1;
-                        x[jj + hstep] = x0 - x1;
-                    }
-                    __syncthreads();
-                }
-                const float sq = 1.0f / sqrtf((float)tb);
-                for (int e = tid; e < hd; e += 256) x[e] *= sq;
-                __syncthreads();
-            }
-        }
-        // RNE Q8_0 quantization of each 32-block, half a wave per block
-        const int hw = tid >> 5, j = tid & 31;
-        for (int bi = hw; bi < G * hd / 32; bi += 8) {
-            const float y = qs_f[bi * 32 + j];
-            float amax = fabsf(y);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            int q = (int)rintf(y * id);
-            q = q < -127 ? -127 : (q > 127 ? 127 : q);
-            qs_i[bi * 32 + j] = (int8_t)q;
-            if (j == 0) qs_d[bi] = d;
-        }
-        __syncthreads();
-    }
-    // this lane's 8 query dims of every head of the group
     float qf[MG][8];
     uint32_t qq[MG][2];
     float qdd[MG];
-#pragma unroll
-    for (int j = 0; j < MG; j++) {
-        const int jj = j < G ? j : 0;
-        if constexpr (KVT == 0) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) qf[j][i] = qs_f[jj * hd + d0 + i];
-        } else {
-            qq[j][0] = *(const uint32_t *)(qs_i + jj * hd + d0);
-            qq[j][1] = *(const uint32_t *)(qs_i + jj * hd + d0 + 4);
-            qdd[j] = qs_d[(jj * hd) / 32 + d0 / 32];
-        }
-    }
+    query_registers<KVT, MG>(a, G, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
     float o[MG][8];
 #pragma unroll
     for (int j = 0; j < MG; j++)
 #pragma unroll
         for (int i = 0; i < 8; i++) o[j][i] = 0.0f;
 
-    const size_t kv_row0 = (size_t)g * a.slots;
     for (int tile = r0; tile < r1; tile += TP) {
-        // ---- K and V of the tile, all loads in flight together ----
-        KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
-        bool ok[ATT_NP];
+        if (tile != r0) load_tile<KVT, PP>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
+        float s4[ATT_NP][MG];
+        tile_scores<KVT, SUB, MG>(kc, qf, qq, qdd, c, cact, d0, s4);
 #pragma unroll
-        for (int n = 0; n < ATT_NP; n++) {
-            const int pos = tile + pi + PP * n;
-            ok[n] = pos < r1;
-            const size_t row = kv_row0 + (size_t)((ok[n] ? pos : r0) % a.slots);
-            load_chunk<KVT>(a.k_cache, a.k_scale, row, hd, d0, tb, kc[n]);
-            load_chunk<KVT>(a.v_cache, a.v_scale, row, hd, d0, tb, vc[n]);
-        }
-        // ---- scores: partial dot over 8 dims, summed over the SUB lanes ----
+        for (int n = 0; n < ATT_NP; n++)
 #pragma unroll
-        for (int n = 0; n < ATT_NP; n++) {
-#pragma unroll
-            for (int j = 0; j < MG; j++) {
-                float part = 0.0f;
-                if constexpr (KVT == 0) {
-                    float kf[8];
-                    chunk_values<0>(kc[n], d0, kf);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) part = fmaf(kf[i], qf[j][i], part);
-                } else {
-                    uint32_t kw[2];
-                    if constexpr (KVT == 1) {
-                        kw[0] = kc[n].raw.x;
-                        kw[1] = kc[n].raw.y;
-                    } else {
-                        turbo_levels8(kc[n], (d0 % 32) >= 16, kw);
-                    }
-                    // the block's integer dot is exact over its 4 lanes (cpu.rs: per-block int32 sums)
-                    const int isum = quad_sum_i(sdot4(kw[1], qq[j][1], sdot4(kw[0], qq[j][0], 0)));
-                    const float ks = KVT == 1 ? h2f(kc[n].sc) : h2f(kc[n].sc) * (1.0f / 46.0f);
-                    part = (cact && (c & 3) == 0) ? (KVT == 1 ? ks * qdd[j] : qdd[j] * ks) * (float)isum : 0.0f;
-                }
-                if (!cact) part = 0.0f;
-                const float sum = group_sum<SUB>(part);
-                if (c == 0 && j < G) sc[j][pi + PP * n] = ok[n] ? softcap_f(sum, a.softcap) : -INFINITY;
-            }
-        }
+            for (int j = 0; j < MG; j++)
+                if (c == 0 && j < G) sc[j][pi + PP * n] = ok[n] ? softcap_f(s4[n][j], a.softcap) : -INFINITY;
         __syncthreads();
         // ---- online softmax: one wavefront per head ----
         const int wv = tid >> 6, lane = tid & 63;
@@ -449,12 +532,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         __syncthreads();
     }
     // ---- sum the position slots: inside the wave, then over the 4 waves in LDS ----
-#pragma unroll
-    for (int off = SUB; off < 64; off <<= 1)
+    xor_up<SUB, 32>([&](auto oc) {
 #pragma unroll
         for (int j = 0; j < MG; j++)
 #pragma unroll
-            for (int i = 0; i < 8; i++) o[j][i] += __shfl_xor(o[j][i], off, 64);
+            for (int i = 0; i < 8; i++) o[j][i] += xor_f<decltype(oc)::value>(o[j][i]);
+    });
     float *wsum = qs_f;  // MG·256 floats: reused, the query now lives in registers
     const int wv = tid >> 6, lane = tid & 63;
     __syncthreads();
@@ -478,6 +561,299 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         pp[hd] = m_run[tid];
         pp[hd + 1] = l_run[tid];
     }
+}
+
+// ---- single token (decode) ----------------------------------------------------------
+// One launch per layer, grid (n_split, n_kv).  The workgroup prepares its group's
+// query heads itself (bias, RMSNorm, RoPE, scale); the workgroup whose range holds
+// the new position also prepares, encodes and appends that position's K and V row
+// and uses its LDS copy of the encoded row.  Each SUB-lane position slot keeps its
+// own online softmax state in registers (no LDS or barrier inside the tile loop);
+// the slots are merged by shuffles within the wave and through LDS across the 4
+// waves.  The last workgroup of each KV head to finish merges the ranges, undoes
+// the Turbo4 rotation and writes att (f32 and Q8_0).
+
+// Merge of the group's n_split range partials by the last workgroup (256 threads).
+// The single-token path keeps scores and running maxima in log2 units (scores
+// scaled by log2 e), so every exponential is one v_exp_f32.
+template <int HD, int G>
+__device__ void combine_group(const AttnArgs &a, int g, float *o_s, float *wts, float *Ls) {
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    constexpr int hd = HD;
+    const int ns = a.n_split;
+    const size_t prow = (size_t)hd + 2;
+    const float *part0 = a.part + (size_t)g * G * ns * prow;
+    constexpr int n_out = G * hd;
+    constexpr int NO = (n_out + 255) / 256;     // outputs per thread
+    constexpr int NPF = NO < 2 ? NO : 2;        // of which the first batch is loaded before the weights
+    constexpr int CB = 16;                      // ranges per batch of loads
+    float pre[NPF][CB];
+#pragma unroll
+    for (int r = 0; r < NPF; r++) {
+        const int i = min(tid + 256 * r, n_out - 1);
+        const float *src = part0 + (size_t)(i / hd) * ns * prow + i % hd;
+#pragma unroll
+        for (int b = 0; b < CB; b++) pre[r][b] = ld_coh(src + (size_t)min(b, ns - 1) * prow);
+    }
+    for (int j = wv; j < G; j += 4) {  // range weights, one wave per head
+        const float *part = part0 + (size_t)j * ns * prow;
+        float mv[ATT_MAX_SPLIT / 64], lv[ATT_MAX_SPLIT / 64];
+#pragma unroll
+        for (int k = 0; k < ATT_MAX_SPLIT / 64; k++) {
+            const int s = min(lane + 64 * k, ns - 1);
+            mv[k] = ld_coh(part + (size_t)s * prow + hd);
+            lv[k] = ld_coh(part + (size_t)s * prow + hd + 1);
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < ATT_MAX_SPLIT / 64; k++) m = fmaxf(m, mv[k]);
+        m = wave_max(m, 64);
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ATT_MAX_SPLIT / 64; k++) {
+            const int s = lane + 64 * k;
+            const float w = (s < ns && lv[k] > 0.0f) ? exp2_hw(mv[k] - m) : 0.0f;
+            if (s < ns) wts[j * ATT_MAX_SPLIT + s] = w;
+            L += s < ns ? lv[k] * w : 0.0f;
+        }
+        L = wave_sum(L, 64);
+        if (lane == 0) Ls[j] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NO; r++) {
+        const int i = min(tid + 256 * r, n_out - 1);
+        const int j = i / hd;
+        const float *src = part0 + (size_t)j * ns * prow + i % hd;
+        const float *w = wts + j * ATT_MAX_SPLIT;
+        float v[CB];
+#pragma unroll
+        for (int b = 0; b < CB; b++) v[b] = r < NPF ? pre[r < NPF ? r : 0][b] : ld_coh(src + (size_t)min(b, ns - 1) * prow);
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < CB; b++)
+            if (b < ns) acc = fmaf(v[b], w[b], acc);
+        for (int s0 = CB; s0 < ns; s0 += CB) {
+#pragma unroll
+            for (int b = 0; b < CB; b++) v[b] = ld_coh(src + (size_t)min(s0 + b, ns - 1) * prow);
+#pragma unroll
+            for (int b = 0; b < CB; b++)
+                if (s0 + b < ns) acc = fmaf(v[b], w[s0 + b], acc);
+        }
+        if (tid + 256 * r < n_out) o_s[i] = acc * (1.0f / Ls[j]);
+    }
+    __syncthreads();
+    if (a.kv_type == 2) {  // o ← Rᵀ o per head: block FWHT, then signs (turbo.rs:114-117)
+        const int b = turbo_block(hd);
+        for (int hstep = 1; hstep < b; hstep *= 2) {
+            for (int k = tid; k < G * hd / 2; k += 256) {
+                const int j = k / (hd / 2), kh = k % (hd / 2);
+                const int blk = kh / (b / 2), kk = kh % (b / 2);
+                const int e = j * hd + blk * b + (kk / hstep) * 2 * hstep + (kk % hstep);
+                const float x0 = o_s[e], x1 = o_s[e + hstep];
+                o_s[e] = x0 + x1;
+                o_s[e + hstep] = x0 - x1;
+            }
+            __syncthreads();
+        }
+        const float sq = 1.0f / sqrtf((float)b);
+        for (int i = tid; i < G * hd; i += 256) o_s[i] = o_s[i] * sq * a.turbo_signs[i % hd];
+        __syncthreads();
+    }
+    const size_t base = (size_t)g * G * hd;
+    for (int i = tid; i < G * hd; i += 256) a.att[base + i] = o_s[i];
+    if (a.att_fmt == ACT_Q8_0) {  // hd % 32 == 0: the group's values are whole blocks
+        const int hw = tid >> 5, j = tid & 31;
+        for (int bi = hw; bi < G * hd / 32; bi += 8) {
+            const float y = o_s[bi * 32 + j];
+            float amax = fabsf(y);
+            amax = xmax_f<32>(amax);
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int q = (int)rintf(y * id);
+            const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
+            int su = q, scl = qc;
+            su = xsum_i<32>(su);
+            scl = xsum_i<32>(scl);
+            const size_t e = base + bi * 32 + j;
+            a.att_q.qs[e] = (int8_t)qc;
+            if (j == 0) {
+                const size_t blk = e / 32;
+                a.att_q.d[blk] = d;
+                if (a.att_q.s) a.att_q.s[blk] = d * (float)su;
+                if (a.att_q.isum) a.att_q.isum[blk] = scl;
+            }
+        }
+    }
+}
+
+
+template <int KVT, int HD, int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepArgs hp) {
+    constexpr int SUB = HD / 8;      // lanes per cache row (8 dims each)
+    constexpr int MG = G;
+    constexpr int PP = 256 / SUB;    // position slots
+    constexpr int TP = PP * ATT_NP;  // positions per tile
+    const int s_idx = blockIdx.x, g = blockIdx.y;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    constexpr int hd = HD;
+    const int p = a.d_pos0 ? *a.d_pos0 : a.pos0;
+    const int start = a.window > 0 ? max(0, p + 1 - a.window) : 0;
+    const int len = p + 1 - start;
+    const int chunk = (len + a.n_split - 1) / a.n_split;
+    const int r0 = start + s_idx * chunk;
+    const int r1 = min(start + (s_idx + 1) * chunk, p + 1);
+    const int pi = tid / SUB, c = tid % SUB;
+    constexpr bool cact = true;
+    const int d0 = 8 * c;
+    constexpr int tb = turbo_block(hd);
+    const bool own = r0 <= p && p < r1;  // this range holds the new position
+
+    __shared__ float qs_f[MG * 256];
+    __shared__ __align__(16) int8_t qs_i[MG * 256];
+    __shared__ float qs_d[MG * 8];
+    __shared__ __align__(16) uint8_t mirror[2][KV_MIRROR_SC + 16];  // the new position's encoded K and V rows
+    __shared__ float pscr[4][520];                                   // per-wave prep scratch
+    __shared__ float wo_s[4][MG * 256];                              // per-wave merged slot states
+    __shared__ float wm_s[4][MG], wl_s[4][MG];
+
+    const size_t kv_row0 = (size_t)g * a.slots;
+    KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
+    bool ok[ATT_NP];
+    if (r0 < r1) load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // overlaps the preparation
+    {
+        const int nv = G + (own ? 2 : 0);
+        for (int v = wv; v < nv; v += 4) {
+            const int kind = v < G ? 0 : v - G + 1;
+            prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
+                           kind == 0 ? nullptr : mirror[kind - 1]);
+        }
+    }
+    __syncthreads();
+    float qf[MG][8];
+    uint32_t qq[MG][2];
+    float qdd[MG];
+    query_registers<KVT, MG>(a, G, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
+
+    float m_s[MG], l_s[MG], o[MG][8];
+#pragma unroll
+    for (int j = 0; j < MG; j++) {
+        m_s[j] = -INFINITY;
+        l_s[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[j][i] = 0.0f;
+    }
+    for (int tile = r0; tile < r1; tile += TP) {
+        if (tile != r0) load_tile<KVT, PP>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
+        if (own && tile + TP >= r1) {
+#pragma unroll
+            for (int n = 0; n < ATT_NP; n++)
+                if (tile + pi + PP * n == p) {
+                    load_chunk<KVT>(mirror[0], (const uint16_t *)(mirror[0] + KV_MIRROR_SC), 0, hd, d0, tb, kc[n]);
+                    load_chunk<KVT>(mirror[1], (const uint16_t *)(mirror[1] + KV_MIRROR_SC), 0, hd, d0, tb, vc[n]);
+                }
+        }
+        float sc[ATT_NP][MG];
+        tile_scores<KVT, SUB, MG>(kc, qf, qq, qdd, c, cact, d0, sc);
+        // online softmax of this slot's positions, per head
+        float pw[ATT_NP][MG];
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int n = 0; n < ATT_NP; n++) {
+                sc[n][j] = ok[n] ? softcap_f(sc[n][j], a.softcap) * LOG2E_F : -INFINITY;
+                mx = fmaxf(mx, sc[n][j]);
+            }
+            const float m_new = fmaxf(m_s[j], mx);
+            const bool any = m_new != -INFINITY;
+            const float al = any ? exp2_hw(m_s[j] - m_new) : 1.0f;
+            float sum = 0.0f;
+#pragma unroll
+            for (int n = 0; n < ATT_NP; n++) {
+                pw[n][j] = any ? exp2_hw(sc[n][j] - m_new) : 0.0f;
+                sum += pw[n][j];
+            }
+            l_s[j] = l_s[j] * al + sum;
+            m_s[j] = m_new;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[j][i] *= al;
+        }
+#pragma unroll
+        for (int n = 0; n < ATT_NP; n++) {
+            float vv[8];
+            chunk_values<KVT>(vc[n], d0, vv);
+#pragma unroll
+            for (int j = 0; j < MG; j++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[j][i] = fmaf(pw[n][j], vv[i], o[j][i]);
+        }
+    }
+    // ---- merge the slots of the wave (lane groups SUB apart) ----
+    xor_up<SUB, 32>([&](auto oc) {
+        constexpr int off = decltype(oc)::value;
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            const float mo = xor_f<off>(m_s[j]), lo = xor_f<off>(l_s[j]);
+            const float M = fmaxf(m_s[j], mo);
+            const bool any = M != -INFINITY;
+            const float a1 = any ? exp2_hw(m_s[j] - M) : 0.0f, a2 = any ? exp2_hw(mo - M) : 0.0f;
+            l_s[j] = l_s[j] * a1 + lo * a2;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[j][i] = o[j][i] * a1 + xor_f<off>(o[j][i]) * a2;
+            m_s[j] = M;
+        }
+    });
+    if (lane < SUB && cact) {
+#pragma unroll
+        for (int j = 0; j < MG; j++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) wo_s[wv][j * hd + d0 + i] = o[j][i];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            wm_s[wv][j] = m_s[j];
+            wl_s[wv][j] = l_s[j];
+        }
+    }
+    __syncthreads();
+    // ---- merge the 4 waves; store this range's partial (agent-coherent) ----
+    const int ns = a.n_split;
+    float *part = a.part + (size_t)g * G * ns * (hd + 2);
+    for (int i = tid; i < G * hd; i += 256) {
+        const int j = i / hd, d = i % hd;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm_s[w][j]);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float aw = M != -INFINITY ? exp2_hw(wm_s[w][j] - M) : 0.0f;
+            O = fmaf(wo_s[w][j * hd + d], aw, O);
+            L = fmaf(wl_s[w][j], aw, L);
+        }
+        float *pp = part + ((size_t)j * ns + s_idx) * (hd + 2);
+        st_coh(pp + d, O);
+        if (d == 0) {
+            st_coh(pp + hd, M);
+            st_coh(pp + hd + 1, L);
+        }
+    }
+    __shared__ int s_last;
+    // Every thread's partial stores have completed (device-visible) before the
+    // barrier, so the arrival count never runs ahead of the data it announces.
+    wait_vmem();
+    __syncthreads();
+    if (tid == 0) {
+        int *cnt = a.counters + g * ATT_CNT_STRIDE;  // one 128-byte line per KV head: no contention between heads
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == ns - 1;
+        if (old == ns - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    combine_group<HD, G>(a, g, qs_f, wo_s[0], wm_s[0]);
 }
 
 // merge the ranges of one (token, head); undo the rotation; quantize to Q8_0
@@ -549,18 +925,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
         for (int bi = hw; bi < hd / 32; bi += 8) {
             const float y = o_s[bi * 32 + j];
             float amax = fabsf(y);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+            amax = xmax_f<32>(amax);
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             const int q = (int)rintf(y * id);
             const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
             int su = q, scl = qc;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) {
-                su += __shfl_xor(su, o, 64);
-                scl += __shfl_xor(scl, o, 64);
-            }
+            su = xsum_i<32>(su);
+            scl = xsum_i<32>(scl);
             const size_t e = (size_t)t * qd + (size_t)h * hd + bi * 32 + j;
             a.att_q.qs[e] = (int8_t)qc;
             if (j == 0) {
@@ -580,11 +952,32 @@ static void launch_split_g(const AttnArgs &a, int G, dim3 grid, hipStream_t st) 
     else hipLaunchKernelGGL((attn_split_kernel<KVT, SUB, 8>), grid, dim3(256), 0, st, a);
 }
 
+template <int KVT, int HD>
+static void launch_decode_g(const AttnArgs &a, const HeadPrepArgs &hp, int G, dim3 grid, hipStream_t st) {
+    switch (G) {
+    case 1: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 1>), grid, dim3(256), 0, st, a, hp); break;
+    case 2: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 2>), grid, dim3(256), 0, st, a, hp); break;
+    case 4: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 4>), grid, dim3(256), 0, st, a, hp); break;
+    default: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 8>), grid, dim3(256), 0, st, a, hp); break;
+    }
+}
+
 template <int KVT>
-static void launch_split_kvt(const AttnArgs &a, dim3 grid, hipStream_t st) {
+static void launch_decode_kvt(const AttnArgs &a, const HeadPrepArgs &hp, dim3 grid, hipStream_t st) {
     const int G = a.n_head / a.n_kv;
-    const int sub = a.hd <= 16 ? 2 : a.hd <= 32 ? 4 : a.hd <= 64 ? 8 : a.hd <= 128 ? 16 : 32;
-    switch (sub) {
+    switch (a.hd) {
+    case 64: launch_decode_g<KVT, 64>(a, hp, G, grid, st); break;
+    case 128: launch_decode_g<KVT, 128>(a, hp, G, grid, st); break;
+    default: launch_decode_g<KVT, 256>(a, hp, G, grid, st); break;
+    }
+}
+
+static int lanes_per_row(int hd) { return hd <= 16 ? 2 : hd <= 32 ? 4 : hd <= 64 ? 8 : hd <= 128 ? 16 : 32; }
+
+template <int KVT>
+static void launch_kvt(const AttnArgs &a, dim3 grid, hipStream_t st) {
+    const int G = a.n_head / a.n_kv;
+    switch (lanes_per_row(a.hd)) {
     case 2: launch_split_g<KVT, 2>(a, G, grid, st); break;
     case 4: launch_split_g<KVT, 4>(a, G, grid, st); break;
     case 8: launch_split_g<KVT, 8>(a, G, grid, st); break;
@@ -595,18 +988,39 @@ static void launch_split_kvt(const AttnArgs &a, dim3 grid, hipStream_t st) {
 
 int attention_splits(int n_tok, int n_kv, int max_len) {
     if (n_tok > 1) return std::max(1, std::min(32, 2048 / std::max(1, n_tok * n_kv)));
-    // decode: at least 32 ranges, and ranges of at most 256 positions
-    return std::min(ATT_MAX_SPLIT, std::max(32, (max_len + 255) / 256));
+    // single token: about 64 positions per range, the count rounded up to a power
+    // of two (so that a captured graph serves a span of context lengths)
+    const int want = (max_len + 63) / 64;
+    int ns = 4;
+    while (ns < want && ns < ATT_MAX_SPLIT) ns *= 2;
+    return ns;
 }
 
 void launch_attention(const AttnArgs &a, hipStream_t st) {
     const dim3 grid(a.n_split, a.n_kv, a.n_tok);
     switch (a.kv_type) {
-    case 0: launch_split_kvt<0>(a, grid, st); break;
-    case 1: launch_split_kvt<1>(a, grid, st); break;
-    default: launch_split_kvt<2>(a, grid, st); break;
+    case 0: launch_kvt<0>(a, grid, st); break;
+    case 1: launch_kvt<1>(a, grid, st); break;
+    default: launch_kvt<2>(a, grid, st); break;
     }
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_head, a.n_tok), dim3(256), 0, st, a);
+}
+
+bool attention_fused_ok(const AttnArgs &a) {
+    const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
+    return a.n_tok == 1 && a.counters && (a.hd == 64 || a.hd == 128 || a.hd == 256) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+           a.n_head == G * a.n_kv && a.n_split <= ATT_MAX_SPLIT;
+}
+
+bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {
+    if (!attention_fused_ok(a) || hp.n_tok != 1) return false;
+    const dim3 grid(a.n_split, a.n_kv, 1);
+    switch (a.kv_type) {
+    case 0: launch_decode_kvt<0>(a, hp, grid, st); break;
+    case 1: launch_decode_kvt<1>(a, hp, grid, st); break;
+    default: launch_decode_kvt<2>(a, hp, grid, st); break;
+    }
+    return true;
 }
 
 }  // namespace rie

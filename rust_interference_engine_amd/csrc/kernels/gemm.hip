@@ -65,7 +65,13 @@ __device__ __forceinline__ void load_wunit(const uint8_t *row, int b, WUnit<TY> 
 // the workgroup stages the activation codes and scales and the weight codes
 // (nibbles kept packed, 16 B/block for Q4_0) and scales in LDS; the next
 // stage's global loads are in flight while the current stage is multiplied.
-constexpr int G_BM = 64, G_BN = 128, G_KC = 4;
+#ifndef RIE_GEMM_KC
+#define RIE_GEMM_KC 4  // 32-value blocks per LDS stage
+#endif
+#ifndef RIE_GEMM_SCALE_MFMA
+#define RIE_GEMM_SCALE_MFMA 1  // d_a·d_w by a rank-1 f32 MFMA (1) or by VALU multiplies (0)
+#endif
+constexpr int G_BM = 64, G_BN = 128, G_KC = RIE_GEMM_KC;
 constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, padded)
 
 template <int TY>
@@ -231,9 +237,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
                                  "v"(dep[6]), "v"(dep[7]), "v"(dep[8]), "v"(dep[9]), "v"(dep[10]), "v"(dep[11]), "v"(dep[12]),
                                  "v"(dep[13]), "v"(dep[14]), "v"(dep[15]));
                     const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw[a], zi, 0, 0, 0);
+#if RIE_GEMM_SCALE_MFMA
                     const v16f Sc = __builtin_amdgcn_mfma_f32_32x32x2f32(as, bs[a], zf, 0, 0, 0);
 #pragma unroll
                     for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)I[v], Sc[v], acc[a][t][v]);
+#else
+                    // lane's weight-row scale × the 16 token scales of this lane (rows 16·(l/32)+v of the tile)
+                    const float dwl = S.dw[a][wrow * G_KC + j];
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        acc[a][t][v] = fmaf((float)I[v], dwl * S.da[(wc * 64 + 32 * t + 16 * h + v) * G_KC + j], acc[a][t][v]);
+#endif
 #pragma unroll
                     for (int v = 0; v < 16; v++) dep[v] = acc[a][t][v];
                 }

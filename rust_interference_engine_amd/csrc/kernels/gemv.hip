@@ -649,7 +649,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
             }
 #pragma unroll
             for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(y[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, xor_f<1>(amax));
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             uint32_t w4[4];
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
                 }
                 w4[j] = v;
             }
-            isum += __shfl_xor(isum, 1, 64);
+            isum += xor_i<1>(isum);
             if (act) {
                 *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
                 if ((tid & 1) == 0) {
@@ -725,11 +725,10 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
             if constexpr (GLU)
                 for (int j = s8; j < LPR; j += 8) sum2 += red[(p.tr + i) * STRIDE + j];
         }
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-            sum += __shfl_xor(sum, o, 64);
-            sum2 += __shfl_xor(sum2, o, 64);
-        }
+        xor_up<1, 4>([&](auto oc) {
+            sum += xor_f<decltype(oc)::value>(sum);
+            sum2 += xor_f<decltype(oc)::value>(sum2);
+        });
         const int r = row0 + i;
         if (s8 == 0 && i < p.tr && r < seg_rows) {
             float v = sum;
@@ -747,18 +746,14 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
         const int r = row0 + tid;
         const float y = r < seg_rows ? hv[tid] : 0.0f;
         float amax = fabsf(y);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        amax = xmax_f<32>(amax);
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int q = (int)rintf(y * id);
         const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
         int su = q, scl = qc;
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) {
-            su += __shfl_xor(su, o, 64);
-            scl += __shfl_xor(scl, o, 64);
-        }
+        su = xsum_i<32>(su);
+        scl = xsum_i<32>(scl);
         if (r < seg_rows) {
             p.hq.qs[r] = (int8_t)qc;
             if ((r & 31) == 0) {

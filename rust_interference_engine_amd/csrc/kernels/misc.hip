@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void argmax_stage1(const float *__restrict__ x
             idx = i;
         }
     }
-    for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
     __shared__ float sv[4];
     __shared__ int si[4];
     if ((tid & 63) == 0) {
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = tid; i < n_part; i += 64) amax_merge(v, idx, pval[i], pidx[i]);
-    for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
     if (tid == 0) *out = idx == 0x7fffffff ? 0u : (uint32_t)idx;
 }
 
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
             for (int q = 0; q < j; q++) taken |= chosen[q] == i;
             if (!taken) amax_merge(v, idx, pr[i], i);
         }
-        for (int o = 32; o > 0; o >>= 1) amax_merge(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+        xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
         if (lane == 0) {
             chosen[j] = idx;
             cval[j] = v;

@@ -60,18 +60,14 @@ __device__ __forceinline__ void quant_q8_0_range(const float *__restrict__ xr, c
         const float y = w ? xv * scale * w[i] : xv;
         if (xn) xn[row * E + i] = y;
         float amax = fabsf(y);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        amax = xmax_f<32>(amax);
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int q = (int)rintf(y * id);
         const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
         int su = q, sc = qc;
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) {
-            su += __shfl_xor(su, o, 64);
-            sc += __shfl_xor(sc, o, 64);
-        }
+        su = xsum_i<32>(su);
+        sc = xsum_i<32>(sc);
         act.qs[row * E + i] = (int8_t)qc;
         if (j == 0) {
             const size_t bi = row * nb + b;
@@ -107,16 +103,16 @@ __device__ __forceinline__ void quant_q8k_range(const float *__restrict__ xr, co
                 mx = y[e];
                 idx = (l << 2) + e;
             }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float oa = __shfl_xor(amax, o, 64), om = __shfl_xor(mx, o, 64);
-            const int oi = __shfl_xor(idx, o, 64);
+        xor_down<32, 1>([&](auto oc) {
+            constexpr int o = decltype(oc)::value;
+            const float oa = xor_f<o>(amax), om = xor_f<o>(mx);
+            const int oi = xor_i<o>(idx);
             if (oa > amax || (oa == amax && oi < idx)) {
                 amax = oa;
                 mx = om;
                 idx = oi;
             }
-        }
+        });
         int8_t *qo = act.qs + row * E + i0;
         const size_t bi = row * nb + b;
         if (amax == 0.0f) {
@@ -134,8 +130,8 @@ __device__ __forceinline__ void quant_q8k_range(const float *__restrict__ xr, co
                 qo[e] = (int8_t)q;
                 s4 += q;
             }
-            s4 += __shfl_xor(s4, 1, 64);
-            s4 += __shfl_xor(s4, 2, 64);
+            s4 += xor_i<1>(s4);
+            s4 += xor_i<2>(s4);
             if ((l & 3) == 0) act.bsums[row * (E >> 4) + (b << 4) + (l >> 2)] = (int16_t)s4;
             if (l == 0) act.d[bi] = 1.0f / iscale;
         }

@@ -362,25 +362,49 @@ def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
     turbo.rs:166-171)."""
     spec, g, _ = _pair(oracle, "qwen3", Q4_0, kv, n_ctx=32, max_batch=4)
     g.set_capture(True)
-    toks = [3, 77, 150, 9]
-    g.forward(toks, 0)
     hd, nkv = spec.head_dim, spec.n_head_kv
-    for layer in range(spec.n_layer):
-        kpost = g.capture(layer, 4, 4 * nkv * hd).reshape(4, nkv, hd)
-        vpost = g.capture(layer, 5, 4 * nkv * hd).reshape(4, nkv, hd)
-        for which, src in ((0, kpost), (1, vpost)):
-            rows, scales = g.kv_layer(layer, which, nkv, 32)
-            for t in range(4):
-                for h in range(nkv):
-                    x = src[t, h]
-                    if kv == 0:
-                        want = x.astype(np.float16).view(np.uint8)
-                        assert np.array_equal(rows[h, t], want)
-                    elif kv == 1:
-                        assert np.array_equal(rows[h, t], oracle.quantize_weights(Q8_0, x))
-                    else:
-                        ref = oracle.turbo_quantize(x)
-                        assert np.array_equal(rows[h, t], ref[2:]) and scales[h, t] == ref[:2].view(np.uint16)[0]
+
+    def check(t0, n):  # cache slots t0..t0+n-1 against the captured rows of the last forward
+        for layer in range(spec.n_layer):
+            kpost = g.capture(layer, 4, n * nkv * hd).reshape(n, nkv, hd)
+            vpost = g.capture(layer, 5, n * nkv * hd).reshape(n, nkv, hd)
+            for which, src in ((0, kpost), (1, vpost)):
+                rows, scales = g.kv_layer(layer, which, nkv, 32)
+                for t in range(n):
+                    for h in range(nkv):
+                        x = src[t, h]
+                        if kv == 0:
+                            want = x.astype(np.float16).view(np.uint8)
+                            assert np.array_equal(rows[h, t0 + t], want)
+                        elif kv == 1:
+                            assert np.array_equal(rows[h, t0 + t], oracle.quantize_weights(Q8_0, x))
+                        else:
+                            ref = oracle.turbo_quantize(x)
+                            assert np.array_equal(rows[h, t0 + t], ref[2:]) and scales[h, t0 + t] == ref[:2].view(np.uint16)[0]
+
+    g.forward([3, 77, 150, 9], 0)   # prompt: separate prep / append launch
+    check(0, 4)
+    for pos, tok in ((4, 41), (5, 6)):  # single tokens: prep and append inside the attention launch
+        g.forward([tok], pos)
+        check(pos, 1)
+
+
+@pytest.mark.parametrize("kv", [0, 1, 2])
+@pytest.mark.parametrize("arch", ["llama", "qwen3"])
+def test_long_decode_matches_oracle(oracle, cuda, arch, kv):
+    """132 single-token steps (query/key prep, cache append, attention and the
+    range merge in one launch) from position 8 to 139: every context length
+    across tile and range boundaries, against the oracle."""
+    from naive_model import max_rel_err
+    spec, g, o = _pair(oracle, arch, Q8_0, kv, n_ctx=160, max_batch=8)
+    nv = spec.n_vocab
+    toks = [(i * 31 + 7) % nv for i in range(140)]
+    g.forward(toks[:8], 0)
+    o.forward(toks[:8], 0)
+    tol = 0.03 if kv == 0 else 0.05
+    for pos in range(8, 140):
+        err = max_rel_err(g.forward([toks[pos]], pos), o.forward([toks[pos]], pos))
+        assert err < tol, f"{arch} kv{kv}: decode position {pos}: {err}"
 
 
 def _top2_margin(x):
