@@ -557,9 +557,11 @@ constexpr int dec_rows_per_pass() {
 
 constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 
-template <int TY, int LPR, int UPL, bool GLU, int R>
-__global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
-    constexpr int GROUPS = 256 / LPR;
+// NT threads (256 or 512): one pass of NT/LPR row groups × R rows covers a
+// 32-row tile in a single pass (all of a workgroup's loads issued up front).
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT>
+__global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
+    constexpr int GROUPS = NT / LPR;
     constexpr int STRIDE = LPR + DEC_PAD;
     constexpr int NW = GLU ? 2 : 1;
     extern __shared__ float red[];  // [NW][tr][STRIDE], then tr floats of h
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
             // thread τ normalizes values 16τ..16τ+15 (a 32-block is a thread pair)
             // into LDS, then every lane reads its slice (quantizer: quant.hip).
             __shared__ __align__(16) int8_t s_q[4096];
-            __shared__ float s_d[128], s_red[4];
+            __shared__ float s_d[128], s_red[NT / 64];
             __shared__ int s_i[128];
             const int K = p.K, nthr = K >> 4;
             const bool act = tid < nthr;
@@ -718,7 +720,7 @@ __global__ __launch_bounds__(256) void gemv_dec_kernel(DecP p) {
     // 8 threads per row add its LPR partials
     float *hv = red + NW * p.tr * STRIDE;
     const int s8 = tid & 7;
-    for (int i = tid >> 3; i < ((p.tr + 31) & ~31); i += 32) {
+    for (int i = tid >> 3; i < ((p.tr + NT / 8 - 1) & ~(NT / 8 - 1)); i += NT / 8) {
         float sum = 0.0f, sum2 = 0.0f;
         if (i < p.tr) {
             for (int j = s8; j < LPR; j += 8) sum += red[i * STRIDE + j];
@@ -799,11 +801,17 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
     while (lpr < U && lpr < 256) lpr *= 2;
     const int upl = (U + lpr - 1) / lpr;
     if (upl > 2) return false;
-    const int pass = (256 / lpr) * R;  // rows per pass of the workgroup
-    int m;
+    int pass = (256 / lpr) * R;  // rows per pass of a 256-thread workgroup
+    int m, nt = 256;
     if (p.glu && p.hq.qs) {
         if (p.total_rows % 32) return false;
-        m = pass >= 32 ? 1 : 32 / pass;  // whole Q8_0 blocks of h per workgroup
+        // whole Q8_0 blocks of h per workgroup, in one pass: 512 or 1024 threads
+        if (pass < 32) {
+            nt = 256 * (32 / pass);
+            pass = 32;
+        }
+        m = 1;
+        if (nt > 1024) return false;
     } else {
         const int ov = dec_tile_override();
         m = ov > 0 ? ov : std::max(1, std::min(4, p.total_rows / (pass * 1024)));
@@ -821,10 +829,12 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         if (i < nseg) blocks += (p.seg[i].rows + p.tr - 1) / p.tr;
         p.blk_end[i] = blocks;
     }
-#define RIE_DEC(L, UP)                                                                        \
-    do {                                                                                      \
-        if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R>), dim3(blocks), dim3(256), lds, st, p);  \
-        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R>), dim3(blocks), dim3(256), lds, st, p);       \
+#define RIE_DEC(L, UP)                                                                                            \
+    do {                                                                                                          \
+        if (p.glu && nt == 512) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 512>), dim3(blocks), dim3(512), lds, st, p);    \
+        else if (p.glu && nt == 1024) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 1024>), dim3(blocks), dim3(1024), lds, st, p); \
+        else if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256>), dim3(blocks), dim3(256), lds, st, p);      \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256>), dim3(blocks), dim3(256), lds, st, p);                \
     } while (0)
     if (upl == 1) {
         switch (lpr) {
