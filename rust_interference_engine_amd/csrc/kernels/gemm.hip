@@ -68,10 +68,7 @@ __device__ __forceinline__ void load_wunit(const uint8_t *row, int b, WUnit<TY> 
 #ifndef RIE_GEMM_KC
 #define RIE_GEMM_KC 4  // 32-value blocks per LDS stage
 #endif
-#ifndef RIE_GEMM_SCALE_MFMA
-#define RIE_GEMM_SCALE_MFMA 1  // d_a·d_w by a rank-1 f32 MFMA (1) or by VALU multiplies (0)
-#endif
-constexpr int G_BM = 64, G_BN = 128, G_KC = RIE_GEMM_KC;
+constexpr int G_BM = 64, G_KC = RIE_GEMM_KC;
 constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, padded)
 
 template <int TY>
@@ -80,34 +77,36 @@ struct GemmLds {
     static constexpr int WST = G_KC * QB + 16;          // weight row stride (bytes, padded)
 };
 
-template <int TY, bool GLU>
+// BN tokens per workgroup tile: 128 (two 32-token tiles per wave) or 64 (one)
+template <int TY, bool GLU, int BN>
 struct __align__(16) GemmStage {
     static constexpr int NW = GLU ? 2 : 1;
-    int8_t a[G_BN * G_AST];
-    float da[G_BN * G_KC];
+    int8_t a[BN * G_AST];
+    float da[BN * G_KC];
     uint8_t wq[NW][G_BM * GemmLds<TY>::WST];
     float dw[NW][G_BM * G_KC];
 };
 
 // registers holding one stage's global loads before they are written to LDS
-template <int TY, bool GLU>
+template <int TY, bool GLU, int BN>
 struct StageRegs {
     static constexpr int NW = GLU ? 2 : 1;
-    v4i a[4];
+    v4i a[BN / 32];  // the thread's part of its token's 128-byte chunk
     float4 da;
     WUnit<TY> w;
 };
 
-template <int TY, bool GLU>
-__device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int t0, int b0, int tid, StageRegs<TY, GLU> &R) {
+template <int TY, bool GLU, int BN>
+__device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int t0, int b0, int tid, StageRegs<TY, GLU, BN> &R) {
     const int K = p.K, nb = K >> 5;
-    {   // activation codes: thread → (token, 64-byte half of the 128-byte chunk)
-        const int tok = min(t0 + (tid >> 1), p.n_tok - 1);
-        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 32 * b0 + 64 * (tid & 1));
+    {   // activation codes: thread → (token, part of its 128-byte chunk)
+        constexpr int TPT = 256 / BN, NV = 128 / TPT / 16;  // threads per token, 16-byte loads per thread
+        const int tok = min(t0 + tid / TPT, p.n_tok - 1);
+        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 32 * b0 + 16 * NV * (tid % TPT));
 #pragma unroll
-        for (int i = 0; i < 4; i++) R.a[i] = src[i];
+        for (int i = 0; i < NV; i++) R.a[i] = src[i];
     }
-    if (tid < G_BN) {
+    if (tid < BN) {
         const int tok = min(t0 + tid, p.n_tok - 1);
         R.da = *(const float4 *)(p.d + (size_t)tok * nb + b0);
     }
@@ -122,14 +121,15 @@ __device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int
     }
 }
 
-template <int TY, bool GLU>
-__device__ __forceinline__ void stage_store(GemmStage<TY, GLU> &S, int tid, const StageRegs<TY, GLU> &R) {
+template <int TY, bool GLU, int BN>
+__device__ __forceinline__ void stage_store(GemmStage<TY, GLU, BN> &S, int tid, const StageRegs<TY, GLU, BN> &R) {
     {
-        v4i *dst = (v4i *)(S.a + (tid >> 1) * G_AST + 64 * (tid & 1));
+        constexpr int TPT = 256 / BN, NV = 128 / TPT / 16;
+        v4i *dst = (v4i *)(S.a + (tid / TPT) * G_AST + 16 * NV * (tid % TPT));
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[i] = R.a[i];
+        for (int i = 0; i < NV; i++) dst[i] = R.a[i];
     }
-    if (tid < G_BN) *(float4 *)(S.da + tid * G_KC) = R.da;
+    if (tid < BN) *(float4 *)(S.da + tid * G_KC) = R.da;
     if (GLU || tid < 128) {
         const int nw = GLU ? (tid >> 7) : 0;
         const int idx = tid & 127, row = idx >> 1, u = idx & 1;
@@ -158,12 +158,12 @@ __device__ __forceinline__ void stage_store(GemmStage<TY, GLU> &S, int tid, cons
     }
 }
 
-template <int TY, bool GLU>
+template <int TY, bool GLU, int NT>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     constexpr int NW = GLU ? 2 : 1;
-    constexpr int NT = 2;  // 32-token tiles per wave
+    constexpr int BN = 64 * NT;  // tokens per workgroup tile: NT 32-token tiles per wave, 2 waves along tokens
     constexpr int QB = GemmLds<TY>::QB, WST = GemmLds<TY>::WST;
-    __shared__ GemmStage<TY, GLU> st[2];
+    __shared__ GemmStage<TY, GLU, BN> st[2];
     const int tid = threadIdx.x;
     const int wv = tid >> 6, l = tid & 63;
     const int wr = wv >> 1, wc = wv & 1;
@@ -175,13 +175,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * G_BM;
-    const int t0 = tg * G_BN;
+    const int t0 = tg * BN;
     const int h = l >> 5, m = l & 31;
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int wrow = wr * 32 + m;  // this lane's weight row in the tile (B operand / result column)
     int arow[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) arow[t] = wc * 64 + 32 * t + tok_m;
+    for (int t = 0; t < NT; t++) arow[t] = wc * 32 * NT + 32 * t + tok_m;
 
     float acc[NW][NT][16];
 #pragma unroll
@@ -193,22 +193,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     const v16i zi = {0};
     const v16f zf = {0};
 
-    float dep[16];
-#pragma unroll
-    for (int v = 0; v < 16; v++) dep[v] = 0.0f;
     const int n_stages = p.K / (32 * G_KC);
-    StageRegs<TY, GLU> R;
-    stage_load<TY, GLU>(p, sg, row0, t0, 0, tid, R);
-    stage_store<TY, GLU>(st[0], tid, R);
+    StageRegs<TY, GLU, BN> R;
+    stage_load<TY, GLU, BN>(p, sg, row0, t0, 0, tid, R);
+    stage_store<TY, GLU, BN>(st[0], tid, R);
     __syncthreads();
+    // Per stage: all operands of the stage's KC blocks from LDS, then the
+    // P = KC·NT·NW tile products in a software pipeline: the MFMAs of product
+    // q+1 are issued before the VALU epilogue of product q.
+    constexpr int P = G_KC * NT * NW;
     for (int s = 0; s < n_stages; s++) {
         const bool more = s + 1 < n_stages;
-        if (more) stage_load<TY, GLU>(p, sg, row0, t0, (s + 1) * G_KC, tid, R);
-        const GemmStage<TY, GLU> &S = st[s & 1];
+        if (more) stage_load<TY, GLU, BN>(p, sg, row0, t0, (s + 1) * G_KC, tid, R);
+        const GemmStage<TY, GLU, BN> &S = st[s & 1];
+        v4i bw[G_KC][NW], av[G_KC][NT];
+        float bs[G_KC][NW], as[G_KC][NT];
 #pragma unroll
         for (int j = 0; j < G_KC; j++) {
-            v4i bw[NW];
-            float bs[NW];
 #pragma unroll
             for (int a = 0; a < NW; a++) {
                 const uint4 q = *(const uint4 *)(S.wq[a] + wrow * WST + j * QB + (TY == T_Q4_0 ? 0 : 16 * h));
@@ -216,44 +217,44 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
                     const uint32_t sh = 4u * (uint32_t)h;
                     const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-                    for (int i = 0; i < 4; i++) bw[a][i] = (int)((((qq[i] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+                    for (int i = 0; i < 4; i++) bw[j][a][i] = (int)((((qq[i] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
                 } else {
-                    bw[a] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                    bw[j][a] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
                 }
-                bs[a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
+                bs[j][a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
             }
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                const v4i av0 = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
-                const float as = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
-#pragma unroll
-                for (int a = 0; a < NW; a++) {
-                    // The empty asm makes this tile's A operand depend on the previous
-                    // tile's finished accumulators: one pair of 32×32 results is live
-                    // at a time (the compiler would otherwise issue every MFMA of the
-                    // stage up front and spill); the SIMD's other waves hide latency.
-                    v4i av = av0;
-                    asm volatile("" : "+v"(av) : "v"(dep[0]), "v"(dep[1]), "v"(dep[2]), "v"(dep[3]), "v"(dep[4]), "v"(dep[5]),
-                                 "v"(dep[6]), "v"(dep[7]), "v"(dep[8]), "v"(dep[9]), "v"(dep[10]), "v"(dep[11]), "v"(dep[12]),
-                                 "v"(dep[13]), "v"(dep[14]), "v"(dep[15]));
-                    const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw[a], zi, 0, 0, 0);
-#if RIE_GEMM_SCALE_MFMA
-                    const v16f Sc = __builtin_amdgcn_mfma_f32_32x32x2f32(as, bs[a], zf, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)I[v], Sc[v], acc[a][t][v]);
-#else
-                    // lane's weight-row scale × the 16 token scales of this lane (rows 16·(l/32)+v of the tile)
-                    const float dwl = S.dw[a][wrow * G_KC + j];
-#pragma unroll
-                    for (int v = 0; v < 16; v++)
-                        acc[a][t][v] = fmaf((float)I[v], dwl * S.da[(wc * 64 + 32 * t + 16 * h + v) * G_KC + j], acc[a][t][v]);
-#endif
-#pragma unroll
-                    for (int v = 0; v < 16; v++) dep[v] = acc[a][t][v];
-                }
+                av[j][t] = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
+                as[j][t] = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
             }
         }
-        if (more) stage_store<TY, GLU>(st[(s + 1) & 1], tid, R);
+        v16i Iq[2];
+        v16f Sq[2];
+        // The MFMAs of product q take an (empty asm) dependency on the finished
+        // accumulators of product q-2: at most two result pairs are live, and the
+        // MFMAs of q overlap the VALU epilogue of q-1.
+        auto issue = [&](int q) {
+            const int j = q / (NT * NW), t = (q / NW) % NT, a = q % NW;
+            v4i aop = av[j][t];
+            if (q >= 2) {
+                const int t2 = ((q - 2) / NW) % NT, a2 = (q - 2) % NW;
+                const float *d = acc[a2][t2];
+                asm volatile("" : "+v"(aop) : "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]), "v"(d[4]), "v"(d[5]), "v"(d[6]), "v"(d[7]),
+                             "v"(d[8]), "v"(d[9]), "v"(d[10]), "v"(d[11]), "v"(d[12]), "v"(d[13]), "v"(d[14]), "v"(d[15]));
+            }
+            Iq[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bw[j][a], zi, 0, 0, 0);
+            Sq[q & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(as[j][t], bs[j][a], zf, 0, 0, 0);
+        };
+        issue(0);
+#pragma unroll
+        for (int q = 0; q < P; q++) {
+            if (q + 1 < P) issue(q + 1);
+            const int t = (q / NW) % NT, a = q % NW;
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)Iq[q & 1][v], Sq[q & 1][v], acc[a][t][v]);
+        }
+        if (more) stage_store<TY, GLU, BN>(st[(s + 1) & 1], tid, R);
         __syncthreads();
     }
     // ---- epilogue: lane holds weight row row0 + wrow for tokens t0 + wc·64 + 32t + 16h + v ----
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int tok = t0 + wc * 64 + 32 * t + 16 * h + v;
+            const int tok = t0 + wc * 32 * NT + 32 * t + 16 * h + v;
             if (tok < p.n_tok) {
                 float y = acc[0][t][v];
                 if constexpr (GLU) y = (p.glu == 2 ? gelu_tanh_f(acc[0][t][v]) : silu_f(acc[0][t][v])) * acc[NW - 1][t][v];
@@ -280,11 +281,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
 
 bool gemm_supported(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % (32 * G_KC) == 0 && K > 0; }
 
+// 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
+// then 64-token tiles (one 32-token tile per wave)
 template <int TY, bool GLU>
 static void launch_t(GemmP p, hipStream_t st) {
-    p.n_tg = (p.n_tok + G_BN - 1) / G_BN;
     const int slots = (p.n_rg + 7) / 8;
-    hipLaunchKernelGGL((gemm_kernel<TY, GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    int nt = 2;
+    if (slots * 8 * ((p.n_tok + 127) / 128) < 512 && p.n_tok > 64) nt = 1;
+    p.n_tg = (p.n_tok + 64 * nt - 1) / (64 * nt);
+    if (nt == 2) hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
 static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }
