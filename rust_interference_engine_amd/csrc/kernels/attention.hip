@@ -13,11 +13,13 @@
 //            f16 scale array [kv_head][slot] (one rotation block for hd=128),
 //            so code rows stay 16-byte aligned.
 // Attention splits each query's context into n_split ranges (flash-decoding):
-// every workgroup handles one (token, kv head, range), keeps the group's query
-// heads in LDS, scores a tile of positions with one lane per position, runs an
-// online softmax and accumulates V with lanes over (head, dim).  A combine
-// kernel merges the ranges, undoes the TurboQuant rotation, and quantizes the
-// result to Q8_0 for the output projection.
+// every workgroup handles one (token, kv head, range) and accumulates V with
+// lanes over (head, dim).  Prompt tokens: the group's query heads sit in LDS,
+// the online softmax runs per tile, and a combine kernel merges the ranges,
+// undoes the TurboQuant rotation and quantizes the result to Q8_0 for the
+// output projection.  A single token: one launch does the query/key
+// preparation, the KV append, the attention and (in the last workgroup of each
+// KV head) the range merge.
 #include "../common.hpp"
 #include "../device.hpp"
 #include "../kernels.hpp"
@@ -316,9 +318,6 @@ __device__ __forceinline__ void chunk_values(const KvChunk<KVT> &c, int d0, floa
     }
 }
 
-// The last workgroup of KV head g to finish merges the n_split ranges of the
-// group's query heads (flash-decoding combine), undoes the TurboQuant rotation
-// and writes att (f32, and Q8_0 when att_fmt asks).  256 threads.
 // Scores of ATT_NP positions × MG query heads: each lane's partial dot over its 8
 // dims, summed over the SUB lanes of the position (every lane of the group gets
 // the sum).  Q8_0 / Turbo4 caches: per-block integer dots (cpu.rs: int32 block

@@ -10,9 +10,8 @@
 //   Q6_K        : one 32-value eighth of a 210-byte superblock (2-byte aligned,
 //                 realigned with v_alignbyte)
 // LPR lanes of a wavefront share a row (64/LPR rows per wave), every weight byte
-// is loaded once per launch with non-temporal loads so the streamed weights do
-// not evict the activations, and a lane's partial sums are reduced across the
-// LPR lanes with cross-lane shuffles.  Per-block integer dot products are exact;
+// is loaded once per launch (plain loads: see wload), and a lane's partial sums
+// are reduced across the LPR lanes through LDS and cross-lane shuffles.  Per-block integer dot products are exact;
 // only the float accumulation order differs from the CPU path.
 #include "../common.hpp"
 #include "../device.hpp"
@@ -64,7 +63,7 @@ struct GemvP {
 // (16..256) share a row so that each lane holds UPL ≤ 2 units.  The lane's
 // activation slice is loaded into registers once and reused for every row of
 // the workgroup; per-lane partial sums go to a padded LDS tile
-// [row][LPR+1] (conflict-free column reads) and one thread per row adds them.
+// [row][LPR+DEC_PAD] and 8 threads per row add them.
 // GLU: gate and up rows give h = act(g)·u, optionally quantized to Q8_0 in the
 // epilogue (32 rows per half-wave) for the down projection.
 // ---------------------------------------------------------------------------
