@@ -81,6 +81,11 @@ void launch_attention(const AttnArgs &a, hipStream_t st);
 // (hp describes the raw Q/K/V rows; hp.q is only read).  False when not applicable.
 bool attention_fused_ok(const AttnArgs &a);
 bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st);
+// ---- attn_prompt.hip ----
+// Prompt batches over an f16 cache on f16 matrix cores (one launch, no range
+// partials); false when the shape or cache type is not covered.
+bool attention_prompt_mfma_ok(const AttnArgs &a);
+bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st);
 // number of context ranges (n_split) for a launch whose longest query sees max_len positions
 constexpr int ATT_MAX_SPLIT = 256;
 int attention_splits(int n_tok, int n_kv, int max_len);

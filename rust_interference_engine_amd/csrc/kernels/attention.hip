@@ -996,6 +996,7 @@ int attention_splits(int n_tok, int n_kv, int max_len) {
 }
 
 void launch_attention(const AttnArgs &a, hipStream_t st) {
+    if (launch_attention_prompt_mfma(a, st)) return;
     const dim3 grid(a.n_split, a.n_kv, a.n_tok);
     switch (a.kv_type) {
     case 0: launch_kvt<0>(a, grid, st); break;

@@ -355,6 +355,45 @@ def test_attention_shapes_match_oracle(oracle, cuda, hd, nh, nkv, kv):
         assert err < tol, f"hd {hd} G {nh // nkv} kv{kv}: decode token {t}: {err}"
 
 
+PROMPT_ATTN_SHAPES = ATTN_SHAPES + [(64, 4, 2), (96, 6, 6)]
+
+
+@pytest.mark.parametrize("hd,nh,nkv", PROMPT_ATTN_SHAPES)
+def test_prompt_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv):
+    """The attention output of prompt batches (f16 cache) against a float64
+    evaluation of cpu.rs:550-634 on the same operands: the prepared queries the
+    GPU used and the f16 cache rows it holds.  Batches start at positions 0, 64
+    and 128 and end inside a 32-position tile, so the causal mask, the tile
+    edges and every query-head grouping are pinned to f32 rounding."""
+    def mut(s):
+        s.head_dim, s.n_head, s.n_head_kv, s.rope_dim = hd, nh, nkv, hd
+    n_ctx = 160
+    spec, g, _ = _pair(oracle, "llama", Q8_0, 0, n_ctx=n_ctx, max_batch=64, mutate=mut)
+    g.set_capture(True)
+    G, qd = nh // nkv, nh * hd
+    toks = [(i * 53 + 11) % spec.n_vocab for i in range(150)]
+    for pos0, end in ((0, 64), (64, 128), (128, 150)):
+        n = end - pos0
+        g.forward(toks[pos0:end], pos0)
+        for layer in range(spec.n_layer):
+            q = g.capture(layer, 3, n * qd).reshape(n, nh, hd).astype(np.float64)
+            att = g.capture(layer, 2, n * qd).reshape(n, nh, hd)
+            kr, _ = g.kv_layer(layer, 0, nkv, n_ctx)
+            vr, _ = g.kv_layer(layer, 1, nkv, n_ctx)
+            K = kr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+            V = vr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+            for t in range(n):
+                p = pos0 + t
+                for hq in range(nh):
+                    kv = hq // G
+                    s = K[kv, :p + 1] @ q[t, hq]
+                    w = np.exp(s - s.max())
+                    ref = (w / w.sum()) @ V[kv, :p + 1]
+                    err = np.max(np.abs(att[t, hq] - ref))
+                    assert err <= 5e-6 * np.max(np.abs(V[kv, :p + 1])) + 1e-6, \
+                        f"hd {hd} G {G} layer {layer} token {p} head {hq}: {err}"
+
+
 @pytest.mark.parametrize("kv", [0, 1, 2])
 def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
     """The cache rows the GPU writes equal the reference encoders applied to the
