@@ -30,7 +30,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 namespace {
 
 constexpr int PT = 32;         // cache positions per tile
-constexpr int VROW = PT * 2 + 16;  // bytes per transposed V row in LDS (padded)
+constexpr int VROW = PT * 2 + 8;   // bytes per transposed V row in LDS (padded: 8-row steps shift by 16 banks)
 
 __device__ __forceinline__ half8 split_hi(const float (&x)[8], half8 &lo) {
     half8 hi;
@@ -44,16 +44,29 @@ __device__ __forceinline__ half8 split_hi(const float (&x)[8], half8 &lo) {
 
 __device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
+// LDS bytes of one wave group's K and transposed V tile
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
+constexpr int tile_bytes() { return PT * (HD * 2 + 16) + HD * VROW; }
+// merge scratch of NW groups: running maxima and sums, then one 32-dim output tile per group
+template <int NW>
+constexpr int merge_bytes() { return NW > 1 ? 2 * NW * 256 * 4 + (NW - 1) * 256 * 16 * 4 : 0; }
+template <int HD, int NW>
+constexpr int prompt_lds_bytes() { return 2 * NW * tile_bytes<HD>() > merge_bytes<NW>() ? 2 * NW * tile_bytes<HD>() : merge_bytes<NW>(); }
+
+// NW groups of 4 waves: group q handles the tiles q, q + NW, …, and the groups'
+// online-softmax states are merged through LDS at the end.
+template <int HD, int NW>
+__global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
     constexpr int KS = HD / 16;          // 16-dim k-steps of the score product
     constexpr int DT = HD / 32;          // 32-dim output tiles
     constexpr int KROW = HD * 2 + 16;    // bytes per K row in LDS (padded)
     constexpr int NCH = (PT * HD / 8 + 255) / 256;  // 16-byte chunks per thread per tile (K and V each)
-    __shared__ __align__(16) uint8_t k_s[PT * KROW];
-    __shared__ __align__(16) uint8_t v_s[HD * VROW];
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int TB = tile_bytes<HD>();
+    const int grp = threadIdx.x >> 8;
+    uint8_t *const tiles = lds + grp * 2 * TB;  // this group's two tile buffers: K rows, then Vᵀ rows
 
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    const int tid = threadIdx.x & 255, wv = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
     const int G = a.n_head / a.n_kv;
     const int wpt = G < 4 ? G : 4;        // waves per 32-token block (query heads side by side)
     const int tbw = 4 / wpt;              // 32-token blocks per workgroup
@@ -84,6 +97,9 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
     const int w_tmin = tb * 32, w_tmax = min(a.n_tok, tb * 32 + 32) - 1;
     const int w_pmax = pos0 + w_tmax;
     const int w_smin = a.window > 0 ? max(0, pos0 + w_tmin + 1 - a.window) : 0;
+    const int w_pmin = pos0 + w_tmin;                                            // the first token's position
+    const int w_smax = a.window > 0 ? max(0, pos0 + w_tmax + 1 - a.window) : 0;  // the last token's window start
+    const bool w_full = wave_on && tb * 32 + 31 < a.n_tok;                        // all 32 tokens exist
 
     // query fragments: token col of the block, dims 16s + 8h .. +8 (f32 → hi + lo)
     half8 qh[KS], ql[KS];
@@ -94,43 +110,56 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
         for (int s = 0; s < KS; s++) {
             const f32x4 x0 = *(const f32x4 *)(qrow + 16 * s + 8 * h);
             const f32x4 x1 = *(const f32x4 *)(qrow + 16 * s + 8 * h + 4);
-            const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
             qh[s] = split_hi(x, ql[s]);
         }
     }
 
     const uint8_t *kc = a.k_cache + (size_t)g * a.slots * (HD * 2);
     const uint8_t *vc = a.v_cache + (size_t)g * a.slots * (HD * 2);
-    u32x4 kr[NCH], vr[NCH];
-    auto fetch = [&](int tile) {
-        const int P0 = k0 + tile * PT;
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            const int ch = tid + 256 * c;
-            const int pos = min(P0 + ch / (HD / 8), p_hi);  // rows past the range repeat a valid one
-            const int slot = pos < a.slots ? pos : pos % a.slots;
-            const size_t off = (size_t)slot * (HD * 2) + (ch % (HD / 8)) * 16;
-            if (ch < PT * HD / 8) {
-                kr[c] = *(const u32x4 *)(kc + off);
-                vr[c] = *(const u32x4 *)(vc + off);
-            }
-        }
+    // one tile in flight in registers: K as 16-byte row chunks, V as two positions × 8 dims
+    struct Regs {
+        u32x4 k[NCH];
+        u32x4 v[2];
     };
-    auto stage = [&]() {
+    // Every lane issues the same loads (indices past the tile's data repeat valid
+    // ones, and ring slots wrap without a branch: slots ≥ 32 = the tile length).
+    auto fetch = [&](int tile, Regs &r) {
+        const int P0 = k0 + tile * PT;
+        const int slot0 = P0 % a.slots;
+        const int span = p_hi - P0;  // positions past p_hi repeat row p_hi
+        auto row = [&](int off) {
+            const int s0 = slot0 + min(off, span);
+            return (size_t)(s0 >= a.slots ? s0 - a.slots : s0) * (HD * 2);
+        };
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int ch = min(tid + 256 * c, PT * HD / 8 - 1);
+            r.k[c] = *(const u32x4 *)(kc + row(ch / (HD / 8)) + (ch % (HD / 8)) * 16);
+        }
+        const int vi = min(tid, 2 * HD - 1);  // positions 2·(vi % 16) + {0, 1}, dims 8·(vi / 16) .. +8
+#pragma unroll
+        for (int rr = 0; rr < 2; rr++) r.v[rr] = *(const u32x4 *)(vc + row(2 * (vi & 15) + rr) + (vi >> 4) * 16);
+    };
+    auto stage = [&](const Regs &r, int buf) {
+        uint8_t *kb = tiles + buf * TB, *vb = kb + PT * KROW;
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
             const int ch = tid + 256 * c;
-            if (ch < PT * HD / 8) {
-                const int p = ch / (HD / 8), d8 = (ch % (HD / 8)) * 8;
-                *(u32x4 *)(k_s + p * KROW + d8 * 2) = kr[c];
-                const uint32_t w[4] = {vr[c][0], vr[c][1], vr[c][2], vr[c][3]};
+            if (ch < PT * HD / 8) *(u32x4 *)(kb + (ch / (HD / 8)) * KROW + (ch % (HD / 8)) * 16) = r.k[c];
+        }
+        if (tid < 2 * HD) {  // Vᵀ[dim][pos]: one dword = the two positions of one dim
+            uint8_t *dst = vb + 8 * (tid >> 4) * VROW + 4 * (tid & 15);
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-                    *(uint16_t *)(v_s + (d8 + i) * VROW + p * 2) = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+            for (int i = 0; i < 8; i++) {
+                const uint32_t w0 = r.v[0][i >> 1], w1 = r.v[1][i >> 1];
+                const uint32_t pair = (i & 1) ? ((w0 >> 16) | (w1 & 0xFFFF0000u)) : ((w0 & 0xFFFFu) | (w1 << 16));
+                *(uint32_t *)(dst + i * VROW) = pair;
             }
         }
     };
 
+    const uint8_t *k_s = tiles, *v_s = tiles + PT * KROW;  // rebound per tile below
     float m = -INFINITY, l_half = 0.0f;
     f32x16 o[DT];
 #pragma unroll
@@ -138,45 +167,76 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; v++) o[d][v] = 0.0f;
 
-    fetch(0);
-    stage();
+    // group tile i is T(i) = grp + i·NW; buffer i & 1 holds T(i) during iteration i, and
+    // the register sets hold T(i+1) and T(i+2) (issued two iterations before their use)
+    const int n_iter = (n_tiles + NW - 1) / NW;
+    // Loads are issued unconditionally (tile indices past the end repeat the last
+    // tile) so that every wait for a register set is an exact count of the loads
+    // issued after it.
+    Regs ra, rb;
+    const int last = n_tiles - 1;
+    fetch(min(grp, last), ra);
+    stage(ra, 0);
+    fetch(min(grp + NW, last), rb);
+    fetch(min(grp + 2 * NW, last), ra);
     __syncthreads();
-    for (int tile = 0; tile < n_tiles; tile++) {
+    auto body = [&](int it, Regs &x) {
+        const int tile = grp + it * NW;
+        stage(x, (it + 1) & 1);
+        fetch(min(tile + 3 * NW, last), x);
+        k_s = tiles + (it & 1) * TB;
+        v_s = k_s + PT * KROW;
         const int P0 = k0 + tile * PT;
-        if (tile + 1 < n_tiles) fetch(tile + 1);
-        const bool work = wave_on && P0 <= w_pmax && P0 + PT - 1 >= w_smin;
+        const bool work = tile < n_tiles && wave_on && P0 <= w_pmax && P0 + PT - 1 >= w_smin;
         if (work) {
-            // Sᵀ[pos][tok] = Σ_d K[pos][d]·q[tok][d]
-            f32x16 s = {};
+            // Sᵀ[pos][tok] = Σ_d K[pos][d]·q[tok][d]; the hi and lo halves of q in two chains
+            f32x16 s = {}, s2 = {};
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const half8 kf = as_half8(*(const u32x4 *)(k_s + col * KROW + (16 * ks + 8 * h) * 2));
                 s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], s, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], s2, 0, 0, 0);
             }
-            // lane: token col, positions P0 + 8(v/4) + 4h + v%4
-            float mx = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int p = P0 + 8 * (v >> 2) + 4 * h + (v & 3);
-                const bool ok = tok_ok && p >= start_t && p <= pos_t;
-                float x = s[v];
-                if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
-                s[v] = ok ? x * LOG2E_F : -INFINITY;
-                mx = fmaxf(mx, s[v]);
+            for (int v = 0; v < 16; v++) s[v] = (s[v] + s2[v]) * LOG2E_F;
+            // lane: token col, positions P0 + 8(v/4) + 4h + v%4; scores in log2 units (q carries log2 e)
+            if (a.softcap > 0.0f) {
+                const float cl = a.softcap * LOG2E_F;  // the cap in the same units
+#pragma unroll
+                for (int v = 0; v < 16; v++) s[v] = cl * tanhf(s[v] / cl);
             }
+            if (!(w_full && P0 + PT - 1 <= w_pmin && P0 >= w_smax)) {  // a tile that is not visible to every token
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int p = P0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    s[v] = (tok_ok && p >= start_t && p <= pos_t) ? s[v] : -INFINITY;
+                }
+            }
+            float mx = s[0];
+#pragma unroll
+            for (int v = 1; v < 16; v++) mx = fmaxf(mx, s[v]);
             mx = fmaxf(mx, xor_f<32>(mx));
-            const float m_new = fmaxf(m, mx);
-            const bool any = m_new != -INFINITY;
-            const float alpha = any ? exp2_hw(m - m_new) : 1.0f;
-            float pv[16], psum = 0.0f;
+            // The reference maximum m moves only when a score exceeds it by more than
+            // 2^8, so probabilities stay ≤ 256 and the accumulators are rescaled rarely
+            // (exact either way: m cancels in O / l).
+            const bool grow = mx > m + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float m_new = grow ? mx : m;
+                const float alpha = grow ? exp2_hw(m - m_new) : 1.0f;  // m = −inf: 0
+                l_half *= alpha;
+#pragma unroll
+                for (int d = 0; d < DT; d++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) o[d][v] *= alpha;
+                m = m_new;
+            }
+            const float mref = m == -INFINITY ? 0.0f : m;  // no visible position yet: every p is 0
+            float pv[16];
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                pv[v] = any ? exp2_hw(s[v] - m_new) : 0.0f;
-                psum += pv[v];
+                pv[v] = exp2_hw(s[v] - mref);
+                l_half += pv[v];
             }
-            l_half = l_half * alpha + psum;
-            m = m_new;
             half8 ph[2], pl[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
@@ -189,8 +249,6 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
             // is position 16u + 4h + i (i < 4) or 16u + 8 + 4h + (i − 4)
 #pragma unroll
             for (int d = 0; d < DT; d++) {
-#pragma unroll
-                for (int v = 0; v < 16; v++) o[d][v] *= alpha;
                 const uint8_t *vrow = v_s + (32 * d + col) * VROW;
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
@@ -208,10 +266,47 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        if (tile + 1 < n_tiles) {
-            stage();
+    };
+    // an even number of steps (the last one may be idle), so that the loop has one
+    // entry path per register set and every wait count is exact
+    for (int it = 0; it < n_iter; it += 2) {
+        body(it, rb);
+        body(it + 1, ra);
+    }
+    if constexpr (NW > 1) {  // merge the groups' states into group 0 (the tile buffers are free now)
+        float *ms = (float *)lds, *ls = ms + NW * 256, *os = ls + NW * 256;
+        ms[grp * 256 + tid] = m;
+        ls[grp * 256 + tid] = l_half;
+        __syncthreads();
+        float M = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < NW; q++) M = fmaxf(M, ms[q * 256 + tid]);
+        const float sc = (M == -INFINITY || m == -INFINITY) ? 0.0f : exp2_hw(m - M);
+        float L = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NW; q++) {
+            const float mq = ms[q * 256 + tid];
+            L += (M == -INFINITY || mq == -INFINITY) ? 0.0f : ls[q * 256 + tid] * exp2_hw(mq - M);
+        }
+        l_half = L;
+#pragma unroll
+        for (int d = 0; d < DT; d++) {
+            if (grp > 0)
+#pragma unroll
+                for (int v = 0; v < 16; v++) os[((grp - 1) * 256 + tid) * 16 + v] = o[d][v] * sc;
+            __syncthreads();
+            if (grp == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    float acc = o[d][v] * sc;
+#pragma unroll
+                    for (int q = 1; q < NW; q++) acc += os[((q - 1) * 256 + tid) * 16 + v];
+                    o[d][v] = acc;
+                }
+            }
             __syncthreads();
         }
+        if (grp > 0) return;
     }
     if (!wave_on) return;
     const float l_tot = l_half + xor_f<32>(l_half);
@@ -271,11 +366,20 @@ __global__ __launch_bounds__(256) void attn_prompt_f16_kernel(AttnArgs a) {
     }
 }
 
+template <int HD, int NW>
+void launch_nw(const AttnArgs &a, dim3 grid, hipStream_t st) {
+    constexpr int lds = prompt_lds_bytes<HD, NW>();
+    static const bool attr = hipFuncSetAttribute((const void *)attn_prompt_f16_kernel<HD, NW>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess;
+    (void)attr;
+    hipLaunchKernelGGL((attn_prompt_f16_kernel<HD, NW>), grid, dim3(256 * NW), lds, st, a);
+}
+
 }  // namespace
 
 bool attention_prompt_mfma_ok(const AttnArgs &a) {
     const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
-    return a.kv_type == 0 && a.n_tok > 1 && !a.d_pos0 && (a.hd == 32 || a.hd == 64 || a.hd == 96 || a.hd == 128) && G >= 1 &&
+    return a.kv_type == 0 && a.n_tok > 1 && !a.d_pos0 && a.slots >= 32 && (a.hd == 32 || a.hd == 64 || a.hd == 96 || a.hd == 128) && G >= 1 &&
            G <= 8 && a.n_head == G * a.n_kv && (a.att_fmt != ACT_Q8_0 || (a.att_q.qs && a.att_q.d));
 }
 
@@ -285,10 +389,10 @@ bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st) {
     const int wpt = G < 4 ? G : 4, tbw = 4 / wpt, hgroups = (G + 3) / 4;
     const dim3 grid((a.n_tok + 32 * tbw - 1) / (32 * tbw), a.n_kv * hgroups);
     switch (a.hd) {
-    case 32: hipLaunchKernelGGL(attn_prompt_f16_kernel<32>, grid, dim3(256), 0, st, a); break;
-    case 64: hipLaunchKernelGGL(attn_prompt_f16_kernel<64>, grid, dim3(256), 0, st, a); break;
-    case 96: hipLaunchKernelGGL(attn_prompt_f16_kernel<96>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(attn_prompt_f16_kernel<128>, grid, dim3(256), 0, st, a); break;
+    case 32: launch_nw<32, 2>(a, grid, st); break;
+    case 64: launch_nw<64, 2>(a, grid, st); break;
+    case 96: launch_nw<96, 2>(a, grid, st); break;
+    default: launch_nw<128, 2>(a, grid, st); break;
     }
     return true;
 }
