@@ -38,9 +38,93 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
     }
 }
 
+// Q8_0 of whole rows, one workgroup per row: thread τ owns values 16τ..16τ+15 of
+// each 4096-value pass (a 32-block is a thread pair), so every load is 16 bytes
+// and every thread writes its 16 codes with one store.  With w, the row is first
+// reduced to its RMSNorm scale and then quantized (second read from L2).
+__global__ __launch_bounds__(256) void q8_0_rows_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w, float eps,
+                                                        int E, float *__restrict__ xn, ActQ8 act) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (size_t)row * ldx;
+    float scale = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int i0 = 16 * tid; i0 < E; i0 += 4096)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float4 v = *(const float4 *)(xr + i0 + 4 * k);
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+        ss = wave_sum(ss, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)E + eps);
+    }
+    for (int base = 0; base < E; base += 4096) {  // uniform trip count: every thread reaches the pair exchanges
+        const int i0 = base + 16 * tid;
+        const bool on = i0 < E;                  // E % 32 == 0: both threads of a pair agree
+        float y[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            if (on) {
+                v = *(const float4 *)(xr + i0 + 4 * k);
+                if (w) g = *(const float4 *)(w + i0 + 4 * k);
+            }
+            y[4 * k] = w ? v.x * scale * g.x : v.x;
+            y[4 * k + 1] = w ? v.y * scale * g.y : v.y;
+            y[4 * k + 2] = w ? v.z * scale * g.z : v.z;
+            y[4 * k + 3] = w ? v.w * scale * g.w : v.w;
+        }
+        if (xn && on)
+#pragma unroll
+            for (int k = 0; k < 4; k++) *(float4 *)(xn + (size_t)row * E + i0 + 4 * k) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(y[e]));
+        amax = fmaxf(amax, xor_f<1>(amax));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t packed[4];
+        int su = 0, sc = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int q = (int)rintf(y[4 * k + e] * id);
+                const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
+                su += q;
+                sc += qc;
+                word |= ((uint32_t)(qc & 0xff)) << (8 * e);
+            }
+            packed[k] = word;
+        }
+        su += xor_i<1>(su);
+        sc += xor_i<1>(sc);
+        if (on) {
+            *(uint4 *)(act.qs + (size_t)row * E + i0) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            if ((tid & 1) == 0) {
+                const size_t bi = ((size_t)row * E + i0) >> 5;
+                act.d[bi] = d;
+                if (act.s) act.s[bi] = d * (float)su;
+                if (act.isum) act.isum[bi] = sc;
+            }
+        }
+    }
+}
+
 void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
                           hipStream_t st) {
     if (fmt == ACT_Q8_0) {
+        if (E % 32 == 0 && ldx % 4 == 0) {
+            hipLaunchKernelGGL(q8_0_rows_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+            return;
+        }
         const int chunks = (E / 32 + Q8_0_BLOCKS_PER_WG - 1) / Q8_0_BLOCKS_PER_WG;
         hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
     } else {
