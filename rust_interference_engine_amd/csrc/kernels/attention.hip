@@ -217,6 +217,116 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
     }
 }
 
+// The same preparation with the head vector in registers (no LDS round trips):
+// HD ∈ {64, 128, 256} with full rotary and an f16 or Q8_0 cache.  Lane l holds
+// elements l + 64k; the NEOX partner e ± HD/2 is in the same lane (HD ≥ 128) or
+// lane l ^ 32 (HD = 64), the interleaved partner e ^ 1 in lane l ^ 1.  The
+// arithmetic is prep_head_wave's, operation for operation.
+__device__ __forceinline__ bool prep_fast_ok(const HeadPrepArgs &a, int hd) {
+    return (hd == 64 || hd == 128 || hd == 256) && a.rope_dim == hd && a.kv_type != 2;
+}
+template <int HD>
+__device__ void prep_head_fast(const HeadPrepArgs &a, int kind, int h, int pos, float *q_dst, uint8_t *mirror) {
+    constexpr int NE = HD / 64, half = HD / 2;
+    const int lane = threadIdx.x & 63;
+    const int qd = a.n_head * HD, kvd = a.n_kv * HD;
+    const float *src = kind == 0 ? a.q + h * HD : (kind == 1 ? a.k : a.v) + h * HD;
+    const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
+    const float *nw = kind == 0 ? a.q_norm : kind == 1 ? a.k_norm : nullptr;
+    (void)qd;
+    (void)kvd;
+    const float *ct = a.cos_t + (size_t)pos * half, *st = a.sin_t + (size_t)pos * half;
+    float x[NE], c[NE], sn[NE];
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int e = lane + 64 * k;
+        x[k] = src[e];
+        const int i = a.neox ? (e < half ? e : e - half) : (e >> 1);
+        c[k] = kind < 2 ? ct[i] : 0.0f;
+        sn[k] = kind < 2 ? st[i] : 0.0f;
+    }
+    if (bias)
+#pragma unroll
+        for (int k = 0; k < NE; k++) x[k] = x[k] + bias[h * HD + lane + 64 * k];
+    if (kind < 2) {
+        if (nw) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NE; k++) ss = fmaf(x[k], x[k], ss);
+            ss = xsum_f<64>(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int k = 0; k < NE; k++) x[k] = x[k] * (scale * nw[lane + 64 * k]);
+        }
+        float y[NE];
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const int e = lane + 64 * k;
+            if (a.neox) {
+                float x0, x1;  // elements i and i + half of the pair
+                if constexpr (HD == 64) {
+                    const float o = xor_f<32>(x[k]);
+                    x0 = e < half ? x[k] : o;
+                    x1 = e < half ? o : x[k];
+                } else {
+                    constexpr int KH = NE / 2;  // element e ± half sits KH slots away in this lane
+                    x0 = k < KH ? x[k] : x[k - KH];
+                    x1 = k < KH ? x[k + KH] : x[k];
+                }
+                y[k] = e < half ? x0 * c[k] - x1 * sn[k] : x0 * sn[k] + x1 * c[k];
+            } else {
+                const float o = xor_f<1>(x[k]);
+                const float x0 = (e & 1) ? o : x[k], x1 = (e & 1) ? x[k] : o;
+                y[k] = (e & 1) == 0 ? x0 * c[k] - x1 * sn[k] : x0 * sn[k] + x1 * c[k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NE; k++) x[k] = y[k];
+    }
+    if (kind == 0) {
+#pragma unroll
+        for (int k = 0; k < NE; k++) q_dst[lane + 64 * k] = x[k] * a.attn_scale;
+        return;
+    }
+    if (a.k_out && kind == 1)
+#pragma unroll
+        for (int k = 0; k < NE; k++) a.k_out[h * HD + lane + 64 * k] = x[k];
+    const size_t row = (size_t)h * a.slots + pos % a.slots;
+    uint8_t *cache = kind == 1 ? a.k_cache : a.v_cache;
+    if (a.kv_type == 0) {
+        uint16_t *dst = (uint16_t *)cache + row * HD;
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const uint16_t hb = f2h(x[k]);
+            dst[lane + 64 * k] = hb;
+            if (mirror) ((uint16_t *)mirror)[lane + 64 * k] = hb;
+        }
+    } else {  // store_q8_0 (cpu.rs:637-647): round half away from zero, f16 scale
+        uint8_t *dst = cache + row * (size_t)(HD / 32 * 34);
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const int e = lane + 64 * k;
+            const float amax = xmax_f<32>(fabsf(x[k]));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            int q = (int)roundf(x[k] * id);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            const int off = (e >> 5) * 34;
+            dst[off + 2 + (e & 31)] = (uint8_t)(int8_t)q;
+            if (mirror) mirror[off + 2 + (e & 31)] = (uint8_t)(int8_t)q;
+            if ((e & 31) == 0) {
+                const uint16_t hb = f2h(d);
+                dst[off] = (uint8_t)hb;
+                dst[off + 1] = (uint8_t)(hb >> 8);
+                if (mirror) {
+                    mirror[off] = (uint8_t)hb;
+                    mirror[off + 1] = (uint8_t)(hb >> 8);
+                }
+            }
+        }
+    }
+}
+
 // one wavefront per (head vector, token); the query is rewritten in place
 __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
     const int t = blockIdx.y;
@@ -722,10 +832,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     if (r0 < r1) load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // overlaps the preparation
     {
         const int nv = G + (own ? 2 : 0);
+        const bool fast = prep_fast_ok(hp, hd);
         for (int v = wv; v < nv; v += 4) {
             const int kind = v < G ? 0 : v - G + 1;
-            prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
-                           kind == 0 ? nullptr : mirror[kind - 1]);
+            if (fast) prep_head_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, qs_f + v * hd, kind == 0 ? nullptr : mirror[kind - 1]);
+            else prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
+                                    kind == 0 ? nullptr : mirror[kind - 1]);
         }
     }
     __syncthreads();
