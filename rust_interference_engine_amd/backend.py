@@ -56,6 +56,7 @@ class HipBackend:
         img = np.frombuffer(gguf, dtype=np.uint8)
         err = C.create_string_buffer(1024)
         code = C.c_int32(0)
+        self._destroy = L.rie_hip_destroy  # held here: module globals may be gone when __del__ runs at exit
         self._h = L.rie_hip_create(img.ctypes.data, img.size, C.byref(cfg), C.byref(code), err, 1024)
         if not self._h:
             raise RieError(code.value, err.value.decode(errors="replace"))
@@ -64,7 +65,7 @@ class HipBackend:
 
     def close(self):
         if getattr(self, "_h", None):
-            _lib.lib().rie_hip_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     __del__ = close

@@ -114,6 +114,12 @@ bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel
 bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
                              const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st);
 
+// ---- gemm_kq.hip (prefill, Q4_K × Q8_K on int8 MFMA; reached through gemm.hip) ----
+bool gemm_kq_supported(int ty, size_t K);
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st);
+bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
+                        hipStream_t st);
+
 // ---- gemm.hip (prefill, int8 MFMA) ----
 bool gemm_supported(int ty, size_t K);
 bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st);

@@ -279,7 +279,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
         }
 }
 
-bool gemm_supported(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % (32 * G_KC) == 0 && K > 0; }
+bool gemm_supported(int ty, size_t K) {
+    return ((ty == T_Q4_0 || ty == T_Q8_0) && K % (32 * G_KC) == 0 && K > 0) || gemm_kq_supported(ty, K);
+}
 
 // 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
 // then 64-token tiles (one 32-token tile per wave)
@@ -307,6 +309,7 @@ static void set_groups(GemmP &p, int nseg) {
 bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st) {
     if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act)) return false;
     const int ty = segs[0].w.ty;
+    if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st);
     GemmP p{};
     for (int i = 0; i < nseg; i++) {
         const GemvSeg &s = segs[i];
@@ -333,6 +336,7 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
 bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
                      float *scratch, hipStream_t st) {
     (void)scratch;
+    if (gemm_kq_supported(gate.ty, K)) return launch_gemm_kq_glu(gate, up, act, n_tok, K, h, ld, gelu, st);
     if (n_tok < 1 || !operands_ok(act) || gate.ty != up.ty || !gemm_supported(gate.ty, K) || gate.cols != (size_t)K ||
         up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
         return false;

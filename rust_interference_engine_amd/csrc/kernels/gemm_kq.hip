@@ -1,0 +1,303 @@
+// gemm_kq.hip — prompt-batch matmul of Q4_K weights × Q8_K activations on CDNA4
+// int8 MFMA, the batched counterpart of the Q4_K block dot (the x86 prefill tiles
+// of kernels/mod.rs:238-296 cover Q4_K; kernels/avx2.rs dot_q4_k 78-107).
+//
+// Per 256-value superblock b, for activation row t and weight row r:
+//   y += (f16(d_r)·d_t)·Σ_j sc_j·Σ_{32} q4·q8 − (f16(dmin_r)·d_t)·Σ_j m_j·(bsum_2j + bsum_2j+1)
+// * the eight 32-value sub-block dots are v_mfma_i32_32x32x32_i8 (exact);
+// * Σ_j sc_j·I_j is an exact int32 sum (|.| < 2^25);
+// * Σ_j m_j·bs_j (< 2^21, exact in f32) and the scale products d·d_t, dmin·d_t are
+//   v_mfma_f32_32x32x2_f32 rank-1 / rank-2 products;
+// so the superblock's two integer sums equal the reference's exactly and only the
+// f32 accumulation over superblocks differs in order.
+//
+// Workgroup tile: 64 weight rows × 64 tokens, 4 waves as 2 × 2 (32 rows × 32
+// tokens each).  A stage is half a superblock (4 sub-blocks, 128 values): the
+// activation codes, the superblock's activation scale and 32-value sums, the
+// weight nibbles of the half and the row's d, dmin and unpacked 6-bit scales and
+// mins go to LDS; the next stage's global loads are in flight meanwhile.
+// Operand lane layout as in gemm.hip: lane l supplies row l mod 32 and values
+// 16·(l/32)..+16; tokens are permuted onto the A rows so that lane l's 16
+// results are the 16 consecutive tokens 16·(l/32) + v.
+#include "../common.hpp"
+#include "../device.hpp"
+#include "../kernels.hpp"
+#include "../gemv_units.hpp"
+
+namespace rie {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+struct KqP {
+    const uint8_t *w[3];
+    size_t rb[3];
+    int rows[3];
+    float *out[3];
+    int ld[3];
+    int epi[3];
+    int nseg;
+    int rg_end[3];  // cumulative 64-row groups at the end of each segment
+    int n_rg, n_tg;
+    int glu;        // 0 none; 1 silu / 2 gelu-tanh: seg 0 gate, seg 1 up, out[0] = h
+    const int8_t *qs;
+    const float *d;
+    const int16_t *bsums;
+    int n_tok, K;
+};
+
+constexpr int KQ_BM = 64, KQ_BN = 64;
+constexpr int KA_ST = 128 + 16;  // activation bytes per token in LDS (one half superblock, padded)
+constexpr int KW_ST = 64 + 16;   // weight nibble bytes per row in LDS (one half superblock, padded)
+
+template <bool GLU>
+struct __align__(16) KqStage {
+    static constexpr int NW = GLU ? 2 : 1;
+    int8_t a[KQ_BN * KA_ST];
+    float da[KQ_BN];
+    float bs[KQ_BN * 8];           // the superblock's 32-value activation sums (both halves hold all 8)
+    uint8_t wq[NW][KQ_BM * KW_ST];
+    float wd[NW][KQ_BM], wdm[NW][KQ_BM];
+    int wsc[NW][KQ_BM * 8];        // 6-bit scales of the 8 sub-blocks
+    float wm[NW][KQ_BM * 8];       // 6-bit mins
+};
+
+struct KqRegs {
+    v4i a[2];         // 32 activation bytes of the thread's token
+    float da;
+    v4i bs[2];        // the token's 16 bsums (int16)
+    v4i wq[2];        // 32 nibble bytes of the thread's row
+    v4i hdr;          // d, dmin, scales[12]
+};
+
+// stage loads for half hs of superblock sb
+template <bool GLU>
+__device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int t0, int sb, int hs, int tid, KqRegs &R) {
+    const int K = p.K, nsb = K >> 8;
+    {
+        const int tok = min(t0 + (tid >> 2), p.n_tok - 1);
+        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 256 * sb + 128 * hs + 32 * (tid & 3));
+        R.a[0] = src[0];
+        R.a[1] = src[1];
+    }
+    if (tid < KQ_BN) {
+        const int tok = min(t0 + tid, p.n_tok - 1);
+        R.da = p.d[(size_t)tok * nsb + sb];
+        const v4i *bsrc = (const v4i *)(p.bsums + (size_t)tok * (K >> 4) + 16 * sb);
+        R.bs[0] = bsrc[0];
+        R.bs[1] = bsrc[1];
+    }
+    if (GLU || tid < 128) {
+        const int nw = GLU ? (tid >> 7) : 0, idx = tid & 127, u = idx & 1;
+        const int s = GLU ? nw : sg;
+        const int row = min(row0 + (idx >> 1), p.rows[GLU ? 0 : sg] - 1);
+        const uint8_t *blk = p.w[s] + (size_t)row * p.rb[s] + 144 * (size_t)sb;
+        const v4i *q = (const v4i *)(blk + 16 + 64 * hs + 32 * u);
+        R.wq[0] = wload(q);
+        R.wq[1] = wload(q + 1);
+        R.hdr = wload((const v4i *)blk);
+    }
+}
+
+template <bool GLU>
+__device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs &R) {
+    {
+        v4i *dst = (v4i *)(S.a + (tid >> 2) * KA_ST + 32 * (tid & 3));
+        dst[0] = R.a[0];
+        dst[1] = R.a[1];
+    }
+    if (tid < KQ_BN) {
+        S.da[tid] = R.da;
+        const uint32_t w[8] = {(uint32_t)R.bs[0][0], (uint32_t)R.bs[0][1], (uint32_t)R.bs[0][2], (uint32_t)R.bs[0][3],
+                               (uint32_t)R.bs[1][0], (uint32_t)R.bs[1][1], (uint32_t)R.bs[1][2], (uint32_t)R.bs[1][3]};
+#pragma unroll
+        for (int j = 0; j < 8; j++)  // bsum_2j + bsum_2j+1 = the two int16 halves of dword j
+            S.bs[tid * 8 + j] = (float)((int)(int16_t)(w[j] & 0xffff) + (int)(int16_t)(w[j] >> 16));
+    }
+    if (GLU || tid < 128) {
+        const int nw = GLU ? (tid >> 7) : 0, idx = tid & 127, row = idx >> 1, u = idx & 1;
+        v4i *dst = (v4i *)(S.wq[nw] + row * KW_ST + 32 * u);
+        dst[0] = R.wq[0];
+        dst[1] = R.wq[1];
+        if (u == 0) {
+            const uint32_t h0 = (uint32_t)R.hdr[0], h1 = (uint32_t)R.hdr[1], h2 = (uint32_t)R.hdr[2], h3 = (uint32_t)R.hdr[3];
+            S.wd[nw][row] = h2f(h0 & 0xffff);
+            S.wdm[nw][row] = h2f(h0 >> 16);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                q4k_scale_min(h1, h2, h3, j, sc, mn);  // get_scale_min_k4 (quant/reference.rs:8-16)
+                S.wsc[nw][row * 8 + j] = sc;
+                S.wm[nw][row * 8 + j] = (float)mn;
+            }
+        }
+    }
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
+    constexpr int NW = GLU ? 2 : 1;
+    __shared__ KqStage<GLU> st[2];
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+    const int wr = wv >> 1, wc = wv & 1;
+    const int bid = blockIdx.x;  // workgroups of one row group share an XCD (id mod 8)
+    const int xcd = bid & 7, u = bid >> 3;
+    const int tg = u % p.n_tg;
+    const int rg = (u / p.n_tg) * 8 + xcd;
+    if (rg >= p.n_rg) return;  // whole workgroup: uniform
+    const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
+    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
+    const int t0 = tg * KQ_BN;
+    const int h = l >> 5, m = l & 31;
+    const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+    const int wrow = wr * 32 + m;   // this lane's weight row (B operand / result column)
+    const int arow = wc * 32 + tok_m;  // this lane's token row of the A operands
+    const v16i zi = {0};
+    const v16f zf = {0};
+
+    float acc[NW][16];
+    int s1[NW][16];
+#pragma unroll
+    for (int a = 0; a < NW; a++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            acc[a][v] = 0.0f;
+            s1[a][v] = 0;
+        }
+    const int n_stages = (p.K >> 8) * 2;
+    KqRegs R;
+    kq_load<GLU>(p, sg, row0, t0, 0, 0, tid, R);
+    kq_store<GLU>(st[0], tid, R);
+    __syncthreads();
+    for (int s = 0; s < n_stages; s++) {
+        const int hs = s & 1;
+        if (s + 1 < n_stages) kq_load<GLU>(p, sg, row0, t0, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        const KqStage<GLU> &S = st[s & 1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const v4i av = *(const v4i *)(S.a + arow * KA_ST + 32 * j + 16 * h);
+#pragma unroll
+            for (int a = 0; a < NW; a++) {
+                const uint4 q = *(const uint4 *)(S.wq[a] + wrow * KW_ST + 32 * (j >> 1) + 16 * h);
+                const uint32_t sh = 4u * (uint32_t)(j & 1);
+                const v4i bw = {(int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu), (int)((q.z >> sh) & 0x0F0F0F0Fu),
+                                (int)((q.w >> sh) & 0x0F0F0F0Fu)};
+                const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, zi, 0, 0, 0);
+                const int sc = S.wsc[a][wrow * 8 + 4 * hs + j];
+#pragma unroll
+                for (int v = 0; v < 16; v++) s1[a][v] += sc * I[v];
+            }
+        }
+        if (hs == 1) {  // end of the superblock: the min term and the two scale products
+#pragma unroll
+            for (int a = 0; a < NW; a++) {
+                v16f s2 = zf;
+#pragma unroll
+                for (int k = 0; k < 4; k++)  // Σ_j m_j·bs_j, sub-blocks 2k + h of each lane half
+                    s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(S.bs[arow * 8 + 2 * k + h], S.wm[a][wrow * 8 + 2 * k + h], s2, 0, 0, 0);
+                const v16f p1 = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? S.da[arow] : 0.0f, h == 0 ? S.wd[a][wrow] : 0.0f, zf, 0, 0, 0);
+                const v16f p2 = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? S.da[arow] : 0.0f, h == 0 ? S.wdm[a][wrow] : 0.0f, zf, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    acc[a][v] += p1[v] * (float)s1[a][v] - p2[v] * s2[v];
+                    s1[a][v] = 0;
+                }
+            }
+        }
+        if (s + 1 < n_stages) kq_store<GLU>(st[(s + 1) & 1], tid, R);
+        __syncthreads();
+    }
+    // ---- epilogue: lane holds weight row row0 + wrow for tokens t0 + wc·32 + 16h + v ----
+    const int rows = p.rows[sg];
+    const int row = row0 + wrow;
+    if (row >= rows) return;
+    float *out = p.out[sg];
+    const int ld = p.ld[sg];
+    const int epi = p.epi[sg];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int tok = t0 + wc * 32 + 16 * h + v;
+        if (tok < p.n_tok) {
+            float y = acc[0][v];
+            if constexpr (GLU) y = (p.glu == 2 ? gelu_tanh_f(acc[0][v]) : silu_f(acc[0][v])) * acc[NW - 1][v];
+            float *o = out + (size_t)tok * ld + row;
+            if (epi == EPI_ADD) *o += y;
+            else *o = y;
+        }
+    }
+}
+
+void kq_groups(KqP &p, int nseg) {
+    int acc = 0;
+    for (int i = 0; i < 3; i++) {
+        if (i < nseg) acc += (p.rows[i] + KQ_BM - 1) / KQ_BM;
+        p.rg_end[i] = acc;
+    }
+    p.n_rg = acc;
+    p.n_tg = (p.n_tok + KQ_BN - 1) / KQ_BN;
+}
+
+template <bool GLU>
+void kq_launch(const KqP &p, hipStream_t st) {
+    const int slots = (p.n_rg + 7) / 8;
+    hipLaunchKernelGGL((gemm_q4k_kernel<GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+}
+
+}  // namespace
+
+bool gemm_kq_supported(int ty, size_t K) { return ty == T_Q4_K && K % 256 == 0 && K > 0; }
+
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st) {
+    if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d || !act.bsums) return false;
+    KqP p{};
+    for (int i = 0; i < nseg; i++) {
+        const GemvSeg &s = segs[i];
+        if (!gemm_kq_supported(s.w.ty, K) || s.w.cols != (size_t)K || !s.w.data || !s.out) return false;
+        p.w[i] = s.w.data;
+        p.rb[i] = s.w.rb();
+        p.rows[i] = (int)s.w.rows;
+        p.out[i] = s.out;
+        p.ld[i] = s.ld;
+        p.epi[i] = s.epi;
+    }
+    p.nseg = nseg;
+    p.n_tok = n_tok;
+    p.K = K;
+    p.qs = act.qs;
+    p.d = act.d;
+    p.bsums = act.bsums;
+    kq_groups(p, nseg);
+    kq_launch<false>(p, st);
+    return true;
+}
+
+bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
+                        hipStream_t st) {
+    if (n_tok < 1 || !act.qs || !act.d || !act.bsums || gate.ty != up.ty || !gemm_kq_supported(gate.ty, K) ||
+        gate.cols != (size_t)K || up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
+        return false;
+    KqP p{};
+    p.w[0] = gate.data;
+    p.w[1] = up.data;
+    p.rb[0] = gate.rb();
+    p.rb[1] = up.rb();
+    p.rows[0] = p.rows[1] = (int)gate.rows;
+    p.out[0] = h;
+    p.ld[0] = ld;
+    p.epi[0] = EPI_STORE;
+    p.nseg = 1;
+    p.glu = gelu ? 2 : 1;
+    p.n_tok = n_tok;
+    p.K = K;
+    p.qs = act.qs;
+    p.d = act.d;
+    p.bsums = act.bsums;
+    kq_groups(p, 1);
+    kq_launch<true>(p, st);
+    return true;
+}
+
+}  // namespace rie

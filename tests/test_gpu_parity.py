@@ -154,16 +154,20 @@ def test_gemv_matches_oracle_rows(oracle, cuda, ty):
                 assert np.all(np.abs(got[t] - want) <= 1e-5 * mag + 1e-6), (ty, k, n_tok)
 
 
-@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0, Q4_K])
 def test_gemm_matches_oracle_rows(oracle, cuda, ty):
     """The int8-MFMA prompt GEMM against the oracle's block dots, for row and
-    token counts that are not multiples of the 32×32 tiles."""
+    token counts that are not multiples of the 32×32 tiles (Q4_K: Q8_K
+    activations, superblock sums with the 6-bit scales and mins)."""
     import ggml_np as G
     r = oracle.Rng(31 + ty)
-    for k, rows, n_tok in ((128, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130)):
+    shapes = ((128, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130))
+    if ty == Q4_K:
+        shapes = ((256, 40, 9), (512, 200, 33), (4096, 96, 70), (1024, 300, 130))
+    for k, rows, n_tok in shapes:
         w = r.random_weight(ty, rows, k)
         x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
-        act = _quant_on_gpu(x, 1, cuda)["dev"]
+        act = _quant_on_gpu(x, act_fmt(ty), cuda)["dev"]
         got = _gemv(ty, w, rows, k, act, None, n_tok, cuda, gemm=True)
         wf = G.dequantize(ty, w, rows * k).reshape(rows, k).astype(np.float64)
         rb = G.row_bytes(ty, k)
@@ -278,7 +282,8 @@ def test_model_logits_match_oracle(oracle, cuda, arch, ty, kv, tol):
         assert err < tol, f"{arch} {ty} kv{kv}: decode token {t}: {err}"
 
 
-@pytest.mark.parametrize("arch,ty", [("llama", Q4_0), ("llama", Q8_0), ("qwen3", Q4_0), ("gemma2", Q8_0)])
+@pytest.mark.parametrize("arch,ty", [("llama", Q4_0), ("llama", Q8_0), ("qwen3", Q4_0), ("gemma2", Q8_0), ("llama", Q4_K),
+                                     ("qwen3", Q4_K)])
 def test_prompt_batches_through_gemm_match_oracle(oracle, cuda, arch, ty):
     """Prompt batches of 24 and 40 tokens run the int8-MFMA GEMM (fused Q/K/V,
     wo, gate/up with SwiGLU/GELU, down) and must match the oracle like decode."""
