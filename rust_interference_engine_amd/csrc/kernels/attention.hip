@@ -225,29 +225,50 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
 __device__ __forceinline__ bool prep_fast_ok(const HeadPrepArgs &a, int hd) {
     return (hd == 64 || hd == 128 || hd == 256) && a.rope_dim == hd && a.kv_type != 2;
 }
+// The loads of one head vector's preparation (the vector, its bias, norm weights
+// and rotary factors), issued apart from the arithmetic so that a caller can put
+// other loads in flight behind them.  kind and h are wave-uniform.
 template <int HD>
-__device__ void prep_head_fast(const HeadPrepArgs &a, int kind, int h, int pos, float *q_dst, uint8_t *mirror) {
+struct PrepIn {
+    static constexpr int NE = HD / 64;
+    float x[NE], c[NE], sn[NE], b[NE], nw[NE];
+};
+template <int HD>
+__device__ __forceinline__ void prep_load_fast(const HeadPrepArgs &a, int kind, int h, int pos, PrepIn<HD> &in) {
     constexpr int NE = HD / 64, half = HD / 2;
     const int lane = threadIdx.x & 63;
-    const int qd = a.n_head * HD, kvd = a.n_kv * HD;
     const float *src = kind == 0 ? a.q + h * HD : (kind == 1 ? a.k : a.v) + h * HD;
     const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
     const float *nw = kind == 0 ? a.q_norm : kind == 1 ? a.k_norm : nullptr;
-    (void)qd;
-    (void)kvd;
     const float *ct = a.cos_t + (size_t)pos * half, *st = a.sin_t + (size_t)pos * half;
-    float x[NE], c[NE], sn[NE];
 #pragma unroll
     for (int k = 0; k < NE; k++) {
         const int e = lane + 64 * k;
-        x[k] = src[e];
+        in.x[k] = src[e];
         const int i = a.neox ? (e < half ? e : e - half) : (e >> 1);
-        c[k] = kind < 2 ? ct[i] : 0.0f;
-        sn[k] = kind < 2 ? st[i] : 0.0f;
+        in.c[k] = kind < 2 ? ct[i] : 0.0f;
+        in.sn[k] = kind < 2 ? st[i] : 0.0f;
+        in.b[k] = bias ? bias[h * HD + e] : 0.0f;
+        in.nw[k] = (kind < 2 && nw) ? nw[e] : 0.0f;
+    }
+}
+
+template <int HD>
+__device__ void prep_finish_fast(const HeadPrepArgs &a, int kind, int h, int pos, const PrepIn<HD> &in, float *q_dst, uint8_t *mirror) {
+    constexpr int NE = HD / 64, half = HD / 2;
+    const int lane = threadIdx.x & 63;
+    const float *bias = kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv;
+    const float *nw = kind == 0 ? a.q_norm : kind == 1 ? a.k_norm : nullptr;
+    float x[NE], c[NE], sn[NE];
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        x[k] = in.x[k];
+        c[k] = in.c[k];
+        sn[k] = in.sn[k];
     }
     if (bias)
 #pragma unroll
-        for (int k = 0; k < NE; k++) x[k] = x[k] + bias[h * HD + lane + 64 * k];
+        for (int k = 0; k < NE; k++) x[k] = x[k] + in.b[k];
     if (kind < 2) {
         if (nw) {
             float ss = 0.0f;
@@ -256,7 +277,7 @@ __device__ void prep_head_fast(const HeadPrepArgs &a, int kind, int h, int pos, 
             ss = xsum_f<64>(ss);
             const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
 #pragma unroll
-            for (int k = 0; k < NE; k++) x[k] = x[k] * (scale * nw[lane + 64 * k]);
+            for (int k = 0; k < NE; k++) x[k] = x[k] * (scale * in.nw[k]);
         }
         float y[NE];
 #pragma unroll
@@ -829,15 +850,35 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     const size_t kv_row0 = (size_t)g * a.slots;
     KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
     bool ok[ATT_NP];
-    if (r0 < r1) load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // overlaps the preparation
-    {
-        const int nv = G + (own ? 2 : 0);
-        const bool fast = prep_fast_ok(hp, hd);
+    // Preparation items: the G query heads, then (range owner only) the new
+    // position's K and V; wave w takes items w, w + 4, ...  On the register path
+    // every item's loads are issued first (clamped to a valid item, so the count
+    // of loads in flight is fixed), then the K/V tile's, and the arithmetic runs
+    // while the tile is in flight.
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
+    const int nv = G + (own ? 2 : 0);
+    const bool fast = prep_fast_ok(hp, hd);
+    constexpr int NI = (G + 2 + 3) / 4;
+    PrepIn<HD> pin[NI];
+    if (fast) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int v = min(wvu + 4 * i, nv - 1), kind = v < G ? 0 : v - G + 1;
+            prep_load_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, pin[i]);
+        }
+    }
+    load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // every row index is in range (mod slots)
+    if (fast) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int v = wvu + 4 * i, kind = v < G ? 0 : v - G + 1;
+            if (v < nv) prep_finish_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, pin[i], qs_f + v * hd, kind == 0 ? nullptr : mirror[kind - 1]);
+        }
+    } else {
         for (int v = wv; v < nv; v += 4) {
             const int kind = v < G ? 0 : v - G + 1;
-            if (fast) prep_head_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, qs_f + v * hd, kind == 0 ? nullptr : mirror[kind - 1]);
-            else prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
-                                    kind == 0 ? nullptr : mirror[kind - 1]);
+            prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
+                               kind == 0 ? nullptr : mirror[kind - 1]);
         }
     }
     __syncthreads();
