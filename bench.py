@@ -40,6 +40,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default: min(16, cores))")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="short run of the roofline kernel (for counters)")
+    ap.add_argument("--long-context", action="store_true",
+                    help="the 32K-context workload instead: pp32768 then tg128 on the same 8B Q4_0 model, Turbo4 and f16 KV")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the forward loop on one GPU; runs on more than one GPU are not part of this build",
@@ -48,6 +50,8 @@ def main():
 
     if args.kernel_only:
         return kernel_only(args)
+    if args.long_context:
+        return long_context(args)
     import torch
 
     import rust_interference_engine_amd as R
@@ -93,6 +97,17 @@ def main():
     tg_tps = args.gen * args.steps / tg_t
     pp_tps = args.prompt * args.steps / pp_t
 
+    # ---- the same 512-token prefill fed in micro-batches of 1, 128 and 512 tokens ----
+    def prefill_batched(b):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for p0 in range(0, args.prompt, b):
+            be.forward_argmax(prompt[p0:p0 + b], p0)
+        torch.cuda.synchronize()
+        return args.prompt / (time.perf_counter() - t)
+    by_batch = {str(b): round(prefill_batched(b), 1) for b in (1, 128)}
+    by_batch[str(args.prompt)] = round(pp_tps, 1)
+
     # ---- roofline of the dominant decode kernel, timed live with HIP events ----
     # (the single-token gate/up/SwiGLU launch over every layer's weights in turn,
     # on the backend's stream, so each launch streams its weights from HBM)
@@ -121,6 +136,7 @@ def main():
         "config": {"workload": "llama-3.1-8b-shaped q4_0, pp512 then greedy tg128, f16 KV", "prompt": args.prompt,
                    "gen": args.gen, "layers": L, "hidden": E, "ffn": FF, "vocab": V, "heads": [spec.n_head, spec.n_head_kv]},
         "pp512_tok_s": round(pp_tps, 1),
+        "prefill_tok_s_by_batch": by_batch,
         "decode_ms_per_token": round(tg_t / (args.gen * args.steps) * 1e3, 4),
         "decode_bytes_per_token": tok_bytes,
         "decode_effective_gbs": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9, 1),
@@ -150,6 +166,44 @@ def measured_traffic():
     except OSError:
         pass
     return None
+
+
+def long_context(args):
+    """The 32K-context workload: the 8B Q4_0 model, a 32768-token prompt fed in
+    512-token batches (Engine::eval_tokens chunking), then 128 greedy steps, with
+    Turbo4 and with f16 KV caches.  One JSON line; not the bench line."""
+    import torch
+
+    import rust_interference_engine_amd as R
+    from rust_interference_engine_amd import synth
+
+    assert torch.cuda.is_available(), "needs the MI355X"
+    n_prompt, n_gen, mb = 32768, 128, 512
+    spec = synth.baseline_llama31_8b_q4_0(seed=1, ctx=n_prompt + n_gen + 128)
+    img = synth.build_array(spec)
+    V = spec.n_vocab
+    prompt = [(i * 7919 + 13) % V for i in range(n_prompt)]
+    res = {}
+    for name, kv in (("turbo4", R.KvType.TURBO4), ("f16", R.KvType.F16)):
+        be = R.HipBackend(img, n_ctx=n_prompt + n_gen + 64, max_batch=mb, kv_type=kv)
+        be.forward_argmax(prompt[:8], 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for p0 in range(0, n_prompt, mb):
+            be.forward_argmax(prompt[p0:p0 + mb], p0)
+            if p0 % (8 * mb) == 0:
+                print(f"{name}: prefilled {p0 + mb} tokens", file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        toks = be.generate_greedy(n_prompt, n_gen)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        res[name] = {"pp32768_tok_s": round(n_prompt / (t1 - t0), 1), "tg128_tok_s": round(n_gen / (t2 - t1), 2),
+                     "kv_bytes": be.kv_bytes(), "greedy_head": [int(t) for t in toks[:8]]}
+        print(f"{name}: {res[name]}", file=sys.stderr, flush=True)
+        be.close()
+    print(json.dumps({"metric": "pp32768 and tg128 tok/s at 32K context (Llama-3.1-8B Q4_0; Turbo4 vs f16 KV)", "n_gpus": 1,
+                      "data": "synthetic: N(0,0.02) weights quantized to Q4_0, prompt ids (i*7919+13) mod V", **res}), flush=True)
 
 
 def kernel_only(args):
