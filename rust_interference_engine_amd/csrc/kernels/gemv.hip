@@ -41,6 +41,7 @@ struct GemvP {
     const float *actf;
     int n_tok, K;
     int glu;  // 0 none, 1 silu, 2 gelu-tanh (seg[0] = gate, seg[1] = up)
+    int tpg;  // tokens per blockIdx.y group (batched GEMV)
 };
 
 // ---------------------------------------------------------------------------
@@ -99,8 +100,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvP p) {
                 sw = p.seg[1].w; srb = p.seg[1].rb; sout = p.seg[1].out; sld = p.seg[1].ld; sepi = p.seg[1].epi;
             }
         }
-        for (int t0 = 0; t0 < p.n_tok; t0 += MAXT) {
-            const int nt = min(MAXT, p.n_tok - t0);
+        const int t_end = min(p.n_tok, ((int)blockIdx.y + 1) * p.tpg);
+        for (int t0 = (int)blockIdx.y * p.tpg; t0 < t_end; t0 += MAXT) {
+            const int nt = min(MAXT, t_end - t0);
             float acc[MAXT] = {0.f, 0.f, 0.f, 0.f};
             float acc2[MAXT] = {0.f, 0.f, 0.f, 0.f};
             if (valid) {
@@ -500,11 +502,19 @@ static void launch_t(const GemvP &p, hipStream_t st) {
     const int waves = (p.total_rows + rpw - 1) / rpw;
     int blocks = (waves + 3) / 4;
     if (blocks > 4096) blocks = 4096;
+    // few rows (a router, a small projection): the tokens are split over
+    // blockIdx.y as well, in groups of a multiple of 4, up to ~1024 workgroups
+    GemvP q = p;
+    int groups = 1;
+    if (blocks < 512 && p.n_tok > 16) groups = std::min((p.n_tok + 15) / 16, std::max(1, 1024 / blocks));
+    q.tpg = ((p.n_tok + groups - 1) / groups + 3) / 4 * 4;
+    groups = (p.n_tok + q.tpg - 1) / q.tpg;
+    const dim3 grid(blocks, groups);
     switch (lpr) {
-    case 8: hipLaunchKernelGGL((gemv_kernel<TY, 8>), dim3(blocks), dim3(256), 0, st, p); break;
-    case 16: hipLaunchKernelGGL((gemv_kernel<TY, 16>), dim3(blocks), dim3(256), 0, st, p); break;
-    case 32: hipLaunchKernelGGL((gemv_kernel<TY, 32>), dim3(blocks), dim3(256), 0, st, p); break;
-    default: hipLaunchKernelGGL((gemv_kernel<TY, 64>), dim3(blocks), dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((gemv_kernel<TY, 8>), grid, dim3(256), 0, st, q); break;
+    case 16: hipLaunchKernelGGL((gemv_kernel<TY, 16>), grid, dim3(256), 0, st, q); break;
+    case 32: hipLaunchKernelGGL((gemv_kernel<TY, 32>), grid, dim3(256), 0, st, q); break;
+    default: hipLaunchKernelGGL((gemv_kernel<TY, 64>), grid, dim3(256), 0, st, q); break;
     }
 }
 

@@ -93,56 +93,64 @@ void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, cons
 // MoE routing (model/cpu.rs:487-501): softmax over the router logits, sort by
 // probability descending with the lower expert index first on ties, keep the
 // top k, optionally renormalize by their sum taken in sorted order.
+// One wave per token, everything in registers: lane l holds experts l + 64i
+// (n_exp ≤ 512, checked by the host).  The softmax sum runs over the experts in
+// order, sequentially, like the reference's (ops.rs:38-49); top-k is k rounds of
+// a wave argmax over the experts not yet taken, the lower index winning ties
+// (cpu.rs:495); lane j keeps the j-th choice and writes it at its rank in
+// ascending expert order (the CPU path adds the experts' outputs in that order,
+// cpu.rs:502-513, and so does launch_moe_combine).
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_exp, int k, int norm_topk, int unit_weights, int *sel,
                                                        float *wgt) {
+    constexpr int NE = 8;
     const int t = blockIdx.x, lane = threadIdx.x;
-    __shared__ float pr[512];
     const float *l = logits + (size_t)t * n_exp;
+    float pr[NE];
     float mx = -INFINITY;
-    for (int i = lane; i < n_exp; i += 64) mx = fmaxf(mx, l[i]);
-    mx = wave_max(mx, 64);
-    for (int i = lane; i < n_exp; i += 64) pr[i] = expf(l[i] - mx);
-    __syncthreads();
-    if (lane == 0) {  // sequential sum and scaling, ops.rs:38-49
-        float sum = 0.0f;
-        for (int i = 0; i < n_exp; i++) sum += pr[i];
-        const float inv = 1.0f / sum;
-        for (int i = 0; i < n_exp; i++) pr[i] *= inv;
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+        const int e = lane + 64 * i;
+        pr[i] = e < n_exp ? l[e] : -INFINITY;
+        mx = fmaxf(mx, pr[i]);
     }
-    __syncthreads();
-    __shared__ int chosen[64];
-    __shared__ float cval[64];
+    mx = wave_max(mx, 64);
+#pragma unroll
+    for (int i = 0; i < NE; i++) pr[i] = lane + 64 * i < n_exp ? expf(pr[i] - mx) : 0.0f;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+        if (64 * i >= n_exp) break;
+        const int nj = min(64, n_exp - 64 * i);
+        for (int j = 0; j < nj; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[i]), j));
+    }
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < NE; i++) pr[i] *= inv;
+    uint32_t taken = 0;  // bit i: expert lane + 64i is chosen
+    int my_c = 0x7fffffff;
+    float my_v = 0.0f, norm = 0.0f;
     for (int j = 0; j < k; j++) {
         float v = -INFINITY;
         int idx = 0x7fffffff;
-        for (int i = lane; i < n_exp; i += 64) {
-            bool taken = false;
-            for (int q = 0; q < j; q++) taken |= chosen[q] == i;
-            if (!taken) amax_merge(v, idx, pr[i], i);
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            const int e = lane + 64 * i;
+            if (e < n_exp && !((taken >> i) & 1u)) amax_merge(v, idx, pr[i], e);
         }
         xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
-        if (lane == 0) {
-            chosen[j] = idx;
-            cval[j] = v;
+        if (idx < n_exp && (idx & 63) == lane) taken |= 1u << (idx >> 6);
+        if (lane == j) {
+            my_c = idx;
+            my_v = v;
         }
-        __syncthreads();
+        norm += v;  // in choice order
     }
-    if (lane == 0) {
-        float norm = 1.0f;
-        if (norm_topk) {
-            norm = 0.0f;
-            for (int j = 0; j < k; j++) norm += cval[j];
-        }
-        // store in ascending expert order: the CPU path adds the experts' outputs
-        // in that order (cpu.rs:502-513), and so does launch_moe_combine
-        for (int j = 0; j < k; j++) {
-            int lo = -1;
-            for (int q = 0; q < k; q++)
-                if (chosen[q] >= 0 && (lo < 0 || chosen[q] < chosen[lo])) lo = q;
-            sel[(size_t)t * k + j] = chosen[lo];
-            wgt[(size_t)t * k + j] = unit_weights ? 1.0f : cval[lo] / norm;
-            chosen[lo] = -1;
-        }
+    if (!norm_topk) norm = 1.0f;
+    int rank = 0;
+    for (int q = 0; q < k; q++) rank += __builtin_amdgcn_readlane(my_c, q) < my_c;
+    if (lane < k) {
+        sel[(size_t)t * k + rank] = my_c;
+        wgt[(size_t)t * k + rank] = unit_weights ? 1.0f : my_v / norm;
     }
 }
 
