@@ -1109,7 +1109,11 @@ static void launch_decode_g(const AttnArgs &a, const HeadPrepArgs &hp, int G, di
     switch (G) {
     case 1: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 1>), grid, dim3(256), 0, st, a, hp); break;
     case 2: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 2>), grid, dim3(256), 0, st, a, hp); break;
+    case 3: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 3>), grid, dim3(256), 0, st, a, hp); break;
     case 4: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 4>), grid, dim3(256), 0, st, a, hp); break;
+    case 5: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 5>), grid, dim3(256), 0, st, a, hp); break;
+    case 6: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 6>), grid, dim3(256), 0, st, a, hp); break;
+    case 7: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 7>), grid, dim3(256), 0, st, a, hp); break;
     default: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 8>), grid, dim3(256), 0, st, a, hp); break;
     }
 }
@@ -1164,8 +1168,8 @@ void launch_attention(const AttnArgs &a, hipStream_t st) {
 
 bool attention_fused_ok(const AttnArgs &a) {
     const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
-    return a.n_tok == 1 && a.counters && (a.hd == 64 || a.hd == 128 || a.hd == 256) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-           a.n_head == G * a.n_kv && a.n_split <= ATT_MAX_SPLIT;
+    return a.n_tok == 1 && a.counters && (a.hd == 64 || a.hd == 128 || a.hd == 256) && G >= 1 && G <= 8 && a.n_head == G * a.n_kv &&
+           a.n_split <= ATT_MAX_SPLIT;
 }
 
 bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {

@@ -328,7 +328,7 @@ def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
 
 
 ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32, query groups 1..8
-    (32, 4, 4), (128, 8, 2), (256, 8, 1), (64, 8, 1), (128, 6, 2),
+    (32, 4, 4), (128, 8, 2), (256, 8, 1), (64, 8, 1), (128, 6, 2), (64, 14, 2), (128, 12, 2),
 ]
 
 
