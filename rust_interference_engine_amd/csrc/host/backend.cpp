@@ -324,7 +324,7 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     const ModelConfig &c = m_.cfg;
     const int E = (int)c.n_embd, ff = (int)L.ff;
     const DevWeight *ws[2] = {&L.gate, &L.up};
-    // single token with Q4_0/Q8_0 gate/up: the gate/up kernel normalizes x itself
+    // single token with Q4_0/Q8_0 or K-quant gate/up: the gate/up kernel normalizes x itself
     const bool self_norm = n == 1 && !capture_ && L.ffn_norm && L.gate.ty == L.up.ty && gemv_norm_ok(L.gate.ty, E);
     const NormIn nin{d_x_, L.ffn_norm, c.rms_eps};
     if (!self_norm) {
@@ -364,9 +364,11 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         const bool swa = c.is_swa(il);
         // ---- attention block ----
         const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
-        // single token with Q4_0/Q8_0 Q/K/V: the GEMV normalizes x itself
+        // single token with Q4_0/Q8_0 or K-quant Q/K/V of one activation format:
+        // the GEMV normalizes and quantizes x itself
+        const int qkv_fmt = act_format(L.wq.ty);
         const bool self_norm = n == 1 && !capture_ && L.attn_norm && gemv_norm_ok(L.wq.ty, E) && gemv_norm_ok(L.wk.ty, E) &&
-                               gemv_norm_ok(L.wv.ty, E);
+                               gemv_norm_ok(L.wv.ty, E) && act_format(L.wk.ty) == qkv_fmt && act_format(L.wv.ty) == qkv_fmt;
         const NormIn nin{d_x_, L.attn_norm, c.rms_eps};
         if (!self_norm) {
             prepare(d_x_, L.attn_norm, n, E, ws, 3, false);
@@ -374,7 +376,8 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         }
         GemvSeg qkv[3] = {{L.wq, d_q_, qd, EPI_STORE}, {L.wk, d_k_, kvd, EPI_STORE}, {L.wv, d_v_, kvd, EPI_STORE}};
         if (self_norm) {
-            if (!launch_gemv(qkv, 3, act0_, d_xn_, n, E, st_, &nin)) throw rt_err("normalizing Q/K/V GEMV launch failed");
+            if (!launch_gemv(qkv, 3, qkv_fmt == ACT_Q8K ? actk_ : act0_, d_xn_, n, E, st_, &nin))
+                throw rt_err("normalizing Q/K/V GEMV launch failed");
             check_launch("matmul");
         } else {
             matmul(qkv, 3, n, E);

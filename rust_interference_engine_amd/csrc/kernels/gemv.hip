@@ -298,6 +298,91 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             }
             have_act = true;
         }
+    } else if constexpr (TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K) {
+        if (p.nin.x) {
+            // The activation is Q8_K(RMSNorm(x)·w), made here once per workgroup in
+            // LDS, in the layout of the global buffer, with the arithmetic of the
+            // standalone quantizer (quant/mod.rs:191-218): the norm's partial sums
+            // in rms_scale_wg's order (the first 256 threads, float4 at 4τ + 1024k);
+            // then 16 threads per superblock, 16 values each: the first strictly
+            // largest |y| (DPP within the 16-lane row, the lower index winning
+            // ties), iscale = −127/max, round-half-away codes, the thread's 16-value
+            // sum, d = 1/iscale.  Every code equals the standalone kernel's.
+            __shared__ __align__(16) int8_t s_q[4096];
+            __shared__ float s_d[16], s_red[4];
+            __shared__ __align__(16) int16_t s_bs[256];
+            const int K = p.K;
+            float ss = 0.0f;
+            if (tid < 256)
+                for (int i = tid * 4; i < K; i += 1024) {
+                    const float4 v = *(const float4 *)(p.nin.x + i);
+                    ss = fmaf(v.x, v.x, ss);
+                    ss = fmaf(v.y, v.y, ss);
+                    ss = fmaf(v.z, v.z, ss);
+                    ss = fmaf(v.w, v.w, ss);
+                }
+            ss = wave_sum(ss, 64);
+            if ((tid & 63) == 0 && tid < 256) s_red[tid >> 6] = ss;
+            __syncthreads();
+            const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+            if (tid < (K >> 4)) {  // whole 16-lane rows
+                float y[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 xv = ((const float4 *)(p.nin.x + 16 * tid))[i], gv = ((const float4 *)(p.nin.w + 16 * tid))[i];
+                    y[4 * i] = xv.x * scale * gv.x;
+                    y[4 * i + 1] = xv.y * scale * gv.y;
+                    y[4 * i + 2] = xv.z * scale * gv.z;
+                    y[4 * i + 3] = xv.w * scale * gv.w;
+                }
+                float am = 0.0f, mv = 0.0f;
+                int idx = 0x7fffffff;
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (fabsf(y[e]) > am) {
+                        am = fabsf(y[e]);
+                        mv = y[e];
+                        idx = 16 * tid + e;
+                    }
+                auto merge = [&](float oa, float om, int oi) {
+                    if (oa > am || (oa == am && oi < idx)) {
+                        am = oa;
+                        mv = om;
+                        idx = oi;
+                    }
+                };
+                merge(dpp_f<DPP_QUAD_XOR1>(am), dpp_f<DPP_QUAD_XOR1>(mv), dpp_i<DPP_QUAD_XOR1>(idx));
+                merge(dpp_f<DPP_QUAD_XOR2>(am), dpp_f<DPP_QUAD_XOR2>(mv), dpp_i<DPP_QUAD_XOR2>(idx));
+                merge(dpp_f<DPP_ROW_ROR4>(am), dpp_f<DPP_ROW_ROR4>(mv), dpp_i<DPP_ROW_ROR4>(idx));
+                merge(dpp_f<DPP_ROW_ROR8>(am), dpp_f<DPP_ROW_ROR8>(mv), dpp_i<DPP_ROW_ROR8>(idx));
+                uint32_t w4[4] = {0u, 0u, 0u, 0u};
+                int bsum = 0;
+                float dsb = 0.0f;
+                if (am != 0.0f) {
+                    const float iscale = -127.0f / mv;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        int q = (int)roundf(iscale * y[e]);
+                        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                        bsum += q;
+                        w4[e >> 2] |= ((uint32_t)(q & 0xff)) << (8 * (e & 3));
+                    }
+                    dsb = 1.0f / iscale;
+                }
+                *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                s_bs[tid] = (int16_t)bsum;
+                if ((tid & 15) == 0) s_d[tid >> 4] = dsb;
+            }
+            __syncthreads();
+            ActQ8 la;
+            la.qs = s_q;
+            la.d = s_d;
+            la.bsums = s_bs;
+#pragma unroll
+            for (int k = 0; k < UPL; k++)
+                if (valid[k]) load_act<TY>(a[k], uu[k], la, nullptr, K, 0);
+            have_act = true;
+        }
     }
     if (!have_act) {
 #pragma unroll
@@ -548,7 +633,11 @@ static bool operands_ok(int ty, const ActQ8 &act, const float *act_f32) {
     }
 }
 
-bool gemv_norm_ok(int ty, size_t K) { return (ty == T_Q4_0 || ty == T_Q8_0) && K % 64 == 0 && K >= 64 && K <= 4096; }
+bool gemv_norm_ok(int ty, size_t K) {
+    if (ty == T_Q4_0 || ty == T_Q8_0) return K % 64 == 0 && K >= 64 && K <= 4096;
+    if (ty == T_Q2_K || ty == T_Q3_K || ty == T_Q4_K || ty == T_Q5_K || ty == T_Q6_K) return K % 256 == 0 && K >= 256 && K <= 4096;
+    return false;
+}
 
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
                  const NormIn *nin) {
