@@ -71,21 +71,59 @@ __device__ __forceinline__ void xor_up(F &&f) {
     }
 }
 
-// butterfly reductions over aligned groups of W lanes (offsets W/2 … 1)
+// ---- DPP lane exchange (VALU, no LDS) ----
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_ROR4 = 0x124;   // row_ror:4 (16-lane rows)
+constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
+constexpr int DPP_HALF_MIRROR = 0x141;  // row_half_mirror (8-lane halves)
+
+// Reductions over aligned groups of W lanes (W = 2..64, a power of two); every
+// lane of the group receives the same result.  Within a 16-lane row: DPP quad
+// exchanges, the 8-lane half mirror and the 8-lane row rotation (VALU, no LDS);
+// across rows: readlane of the row results, combined in a fixed order.  The
+// partner lanes are the group's own, so the group must be active.
+template <int W, class T, class Op>
+__device__ __forceinline__ T xreduce(T v, Op op) {
+    static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    auto dpp = [](T x, auto ctrl) {
+        if constexpr (sizeof(T) == 4 && std::is_same_v<T, float>) return dpp_f<decltype(ctrl)::value>(x);
+        else return dpp_i<decltype(ctrl)::value>(x);
+    };
+    v = op(v, dpp(v, std::integral_constant<int, DPP_QUAD_XOR1>{}));
+    if constexpr (W >= 4) v = op(v, dpp(v, std::integral_constant<int, DPP_QUAD_XOR2>{}));
+    if constexpr (W >= 8) v = op(v, dpp(v, std::integral_constant<int, DPP_HALF_MIRROR>{}));
+    if constexpr (W >= 16) v = op(v, dpp(v, std::integral_constant<int, DPP_ROW_ROR8>{}));
+    if constexpr (W >= 32) {
+        auto rl = [&](int ln) {
+            if constexpr (std::is_same_v<T, float>) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), ln));
+            else return (T)__builtin_amdgcn_readlane((int)v, ln);
+        };
+        const T r0 = rl(0), r1 = rl(16), r2 = rl(32), r3 = rl(48);
+        if constexpr (W == 32) v = (__lane_id() < 32) ? op(r0, r1) : op(r2, r3);
+        else v = op(op(r0, r1), op(r2, r3));
+    }
+    return v;
+}
 template <int W>
 __device__ __forceinline__ float xsum_f(float v) {
-    xor_down<W / 2, 1>([&](auto o) { v += xor_f<decltype(o)::value>(v); });
-    return v;
+    return xreduce<W>(v, [](float a, float b) { return a + b; });
 }
 template <int W>
 __device__ __forceinline__ int xsum_i(int v) {
-    xor_down<W / 2, 1>([&](auto o) { v += xor_i<decltype(o)::value>(v); });
-    return v;
+    return xreduce<W>(v, [](int a, int b) { return a + b; });
 }
 template <int W>
 __device__ __forceinline__ float xmax_f(float v) {
-    xor_down<W / 2, 1>([&](auto o) { v = fmaxf(v, xor_f<decltype(o)::value>(v)); });
-    return v;
+    return xreduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 __device__ __forceinline__ float wave_sum(float v, int width) {
@@ -132,20 +170,6 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
     return 0.5f * x * (1.0f + tanhf(k * x * (1.0f + 0.044715f * x * x)));
 }
 
-// ---- DPP lane exchange (VALU, no LDS) ----
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
-constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
-constexpr int DPP_ROW_ROR4 = 0x124;   // row_ror:4 (16-lane rows)
-constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
-constexpr int DPP_HALF_MIRROR = 0x141;  // row_half_mirror (8-lane halves)
 
 // Sum over aligned groups of W lanes (W = 1..32, a power of two); every lane of
 // the group receives the sum.  Call with the whole wavefront active.
