@@ -42,13 +42,16 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return b;
 }
 
-// Value held by lane (this lane xor OFF): one ds_swizzle (bitmask mode, within a
-// 32-lane half) for OFF < 32, one ds_bpermute for OFF = 32; no per-call lane-id
-// arithmetic.  Call with the source lanes active.
+// Value held by lane (this lane xor OFF): a DPP quad permutation for OFF = 1, 2
+// (VALU), one ds_swizzle (bitmask mode, within a 32-lane half) for OFF = 4..16,
+// one ds_bpermute for OFF = 32; no per-call lane-id arithmetic.  Call with the
+// source lanes active.
 template <int OFF>
 __device__ __forceinline__ int xor_i(int v) {
     static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane offset");
-    if constexpr (OFF == 32) return __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), v);
+    if constexpr (OFF == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    else if constexpr (OFF == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else if constexpr (OFF == 32) return __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), v);
     else return __builtin_amdgcn_ds_swizzle(v, 0x1F | (OFF << 10));
 }
 template <int OFF>
