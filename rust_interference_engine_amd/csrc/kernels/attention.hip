@@ -28,7 +28,24 @@
 
 namespace rie {
 
-__constant__ int8_t KV_LEVELS_I8[16] = {-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126};
+// Lloyd–Max levels of the 4-bit Turbo4 codes as int8 (turbo.rs:126-127), and the
+// same 16 bytes as four little-endian dwords for v_perm table lookups
+constexpr int8_t KV_LEVELS_I8[16] = {-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126};
+constexpr uint32_t kv_level_word(int i) {
+    return (uint32_t)(uint8_t)KV_LEVELS_I8[4 * i] | ((uint32_t)(uint8_t)KV_LEVELS_I8[4 * i + 1] << 8) |
+           ((uint32_t)(uint8_t)KV_LEVELS_I8[4 * i + 2] << 16) | ((uint32_t)(uint8_t)KV_LEVELS_I8[4 * i + 3] << 24);
+}
+constexpr uint32_t KV_LV0 = kv_level_word(0), KV_LV1 = kv_level_word(1), KV_LV2 = kv_level_word(2), KV_LV3 = kv_level_word(3);
+
+// four table lookups: byte i of s (each 0..15) → byte s_i of the 16-byte table t0..t3
+// (v_perm selects among 8 bytes; selector 12 gives 0x00 and 13 gives 0xFF, which
+// makes the byte mask of s_i ≥ 8)
+__device__ __forceinline__ uint32_t lut16(uint32_t s, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t s7 = s & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, s7), hi = __builtin_amdgcn_perm(t3, t2, s7);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((s >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+    return (hi & m) | (lo & ~m);
+}
 
 __host__ __device__ constexpr int turbo_block(int d) {
     int b = 1;
@@ -415,14 +432,8 @@ __device__ __forceinline__ void turbo_levels8(const KvChunk<2> &c, bool hi, uint
     const uint32_t w[2] = {c.raw.x, c.raw.y};
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        uint32_t r = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t byte = (w[h] >> (8 * i)) & 0xff;
-            const uint32_t code = hi ? (byte >> 4) : (byte & 15);
-            r |= ((uint32_t)(uint8_t)KV_LEVELS_I8[code]) << (8 * i);
-        }
-        out[h] = r;
+        const uint32_t codes = (hi ? (w[h] >> 4) : w[h]) & 0x0F0F0F0Fu;  // one code per byte
+        out[h] = lut16(codes, KV_LV0, KV_LV1, KV_LV2, KV_LV3);
     }
 }
 
