@@ -415,10 +415,9 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             if constexpr (GLU)
                 for (int j = s8; j < LPR; j += 8) sum2 += red[(p.tr + i) * STRIDE + j];
         }
-        xor_up<1, 4>([&](auto oc) {
-            sum += xor_f<decltype(oc)::value>(sum);
-            sum2 += xor_f<decltype(oc)::value>(sum2);
-        });
+        // the 8 lanes of the row (DPP: the same pairings as a 1, 2, 4 butterfly)
+        sum = xsum_f<8>(sum);
+        sum2 = xsum_f<8>(sum2);
         const int r = row0 + i;
         if (s8 == 0 && i < p.tr && r < seg_rows) {
             float v = sum;
