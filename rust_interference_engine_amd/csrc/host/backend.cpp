@@ -216,7 +216,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     actk_.bsums = dalloc<int16_t>(allocs_, kq / 16);
     part_floats_ = (size_t)std::max<size_t>(32 * mb, ATT_MAX_SPLIT) * c.n_head * (hd + 2);
     d_part_ = dalloc<float>(allocs_, part_floats_);
-    d_attn_cnt_ = dalloc<int>(allocs_, c.n_head_kv * ATT_CNT_STRIDE);
+    d_attn_cnt_ = dalloc<int>(allocs_, c.n_head * ATT_CNT_STRIDE);  // one per head slice: at most one per query head
     d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
     if (c.n_expert) {
@@ -425,7 +425,16 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         aa.counters = d_attn_cnt_;
         // single token: prep, append, attention and range merge in one launch
         const bool fused_attn = n == 1 && attention_fused_ok(aa);
-        if (!fused_attn) {
+        // capture also runs the standalone prep before the fused launch, for its
+        // query rows; that prep works on the query in place, so the raw rows are
+        // put back for the fused kernel (which rewrites the same cache row, same bytes)
+        if (!fused_attn || (capture_ && !in_capture_)) {
+            std::vector<float> raw_q;
+            if (fused_attn) {
+                RIE_HIP_CHECK(hipStreamSynchronize(st_));
+                raw_q.resize((size_t)n * qd);
+                RIE_HIP_CHECK(hipMemcpy(raw_q.data(), d_q_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
+            }
             launch_head_prep(hp, st_);
             check_launch("head_prep");
             mark("head_prep_kv_append");
@@ -435,6 +444,7 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
                 cap_[3][il].resize((size_t)n * qd);
                 RIE_HIP_CHECK(hipMemcpy(cap_[3][il].data(), d_q_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
             }
+            if (fused_attn) RIE_HIP_CHECK(hipMemcpy(d_q_, raw_q.data(), (size_t)n * qd * 4, hipMemcpyHostToDevice));
         }
         if (fused_attn) {
             if (!launch_attention_fused(aa, hp, st_)) throw rt_err("fused attention launch rejected");

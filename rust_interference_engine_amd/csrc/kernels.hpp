@@ -73,9 +73,9 @@ struct AttnArgs {
     int att_fmt;
     const int *d_pos0;
     const float *turbo_signs;
-    int *counters;               // fused single-token path: [n_kv · ATT_CNT_STRIDE] zeroed ints, left zeroed
+    int *counters;               // fused single-token path: [n_head · ATT_CNT_STRIDE] zeroed ints, left zeroed
 };
-constexpr int ATT_CNT_STRIDE = 32;  // ints between the per-KV-head arrival counters
+constexpr int ATT_CNT_STRIDE = 32;  // ints between the arrival counters of the head slices
 void launch_attention(const AttnArgs &a, hipStream_t st);
 // Single token: Q/K prep, KV append, attention and the range merge in one launch
 // (hp describes the raw Q/K/V rows; hp.q is only read).  False when not applicable.

@@ -714,16 +714,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // waves.  The last workgroup of each KV head to finish merges the ranges, undoes
 // the Turbo4 rotation and writes att (f32 and Q8_0).
 
-// Merge of the group's n_split range partials by the last workgroup (256 threads).
+// Merge of the n_split range partials of query heads h0 .. h0 + G - 1 by the last
+// workgroup (256 threads).
 // The single-token path keeps scores and running maxima in log2 units (scores
 // scaled by log2 e), so every exponential is one v_exp_f32.
 template <int HD, int G>
-__device__ void combine_group(const AttnArgs &a, int g, float *o_s, float *wts, float *Ls) {
+__device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts, float *Ls) {
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     constexpr int hd = HD;
     const int ns = a.n_split;
     const size_t prow = (size_t)hd + 2;
-    const float *part0 = a.part + (size_t)g * G * ns * prow;
+    const float *part0 = a.part + (size_t)h0 * ns * prow;
     constexpr int n_out = G * hd;
     constexpr int NO = (n_out + 255) / 256;     // outputs per thread
     constexpr int NPF = NO < 2 ? NO : 2;        // of which the first batch is loaded before the weights
@@ -801,7 +802,7 @@ __device__ void combine_group(const AttnArgs &a, int g, float *o_s, float *wts, 
         for (int i = tid; i < G * hd; i += 256) o_s[i] = o_s[i] * sq * a.turbo_signs[i % hd];
         __syncthreads();
     }
-    const size_t base = (size_t)g * G * hd;
+    const size_t base = (size_t)h0 * hd;
     for (int i = tid; i < G * hd; i += 256) a.att[base + i] = o_s[i];
     if (a.att_fmt == ACT_Q8_0) {  // hd % 32 == 0: the group's values are whole blocks
         const int hw = tid >> 5, j = tid & 31;
@@ -829,13 +830,17 @@ __device__ void combine_group(const AttnArgs &a, int g, float *o_s, float *wts, 
 }
 
 
-template <int KVT, int HD, int G>
+// G query heads share a KV head; a workgroup takes H of them (H divides G), so the
+// grid is (n_split, n_kv · G / H): blockIdx.y = g · (G / H) + the head slice.
+template <int KVT, int HD, int G, int H>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepArgs hp) {
+    static_assert(G % H == 0, "the head slices tile the group");
     constexpr int SUB = HD / 8;      // lanes per cache row (8 dims each)
-    constexpr int MG = G;
+    constexpr int MG = H;
     constexpr int PP = 256 / SUB;    // position slots
     constexpr int TP = PP * ATT_NP;  // positions per tile
-    const int s_idx = blockIdx.x, g = blockIdx.y;
+    const int s_idx = blockIdx.x, g = blockIdx.y / (G / H);
+    const int h0 = g * G + (blockIdx.y % (G / H)) * H;  // first query head of the slice
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     constexpr int hd = HD;
     const int p = a.d_pos0 ? *a.d_pos0 : a.pos0;
@@ -861,34 +866,36 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     const size_t kv_row0 = (size_t)g * a.slots;
     KvChunk<KVT> kc[ATT_NP], vc[ATT_NP];
     bool ok[ATT_NP];
-    // Preparation items: the G query heads, then (range owner only) the new
-    // position's K and V; wave w takes items w, w + 4, ...  On the register path
+    // Preparation items: the H query heads, then (range owner only) the new
+    // position's K and V; wave w takes items w, w + 4, ...  When a group is split
+    // into slices, each slice's range owner writes the same encoded row to the
+    // cache (identical bytes) and keeps its own LDS copy.  On the register path
     // every item's loads are issued first (clamped to a valid item, so the count
     // of loads in flight is fixed), then the K/V tile's, and the arithmetic runs
     // while the tile is in flight.
     const int wvu = __builtin_amdgcn_readfirstlane(wv);
-    const int nv = G + (own ? 2 : 0);
+    const int nv = H + (own ? 2 : 0);
     const bool fast = prep_fast_ok(hp, hd);
-    constexpr int NI = (G + 2 + 3) / 4;
+    constexpr int NI = (H + 2 + 3) / 4;
     PrepIn<HD> pin[NI];
     if (fast) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int v = min(wvu + 4 * i, nv - 1), kind = v < G ? 0 : v - G + 1;
-            prep_load_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, pin[i]);
+            const int v = min(wvu + 4 * i, nv - 1), kind = v < H ? 0 : v - H + 1;
+            prep_load_fast<HD>(hp, kind, kind == 0 ? h0 + v : g, p, pin[i]);
         }
     }
     load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // every row index is in range (mod slots)
     if (fast) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int v = wvu + 4 * i, kind = v < G ? 0 : v - G + 1;
-            if (v < nv) prep_finish_fast<HD>(hp, kind, kind == 0 ? g * G + v : g, p, pin[i], qs_f + v * hd, kind == 0 ? nullptr : mirror[kind - 1]);
+            const int v = wvu + 4 * i, kind = v < H ? 0 : v - H + 1;
+            if (v < nv) prep_finish_fast<HD>(hp, kind, kind == 0 ? h0 + v : g, p, pin[i], qs_f + v * hd, kind == 0 ? nullptr : mirror[kind - 1]);
         }
     } else {
         for (int v = wv; v < nv; v += 4) {
-            const int kind = v < G ? 0 : v - G + 1;
-            prep_head_wave<HD>(hp, kind, kind == 0 ? g * G + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
+            const int kind = v < H ? 0 : v - H + 1;
+            prep_head_wave<HD>(hp, kind, kind == 0 ? h0 + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
                                kind == 0 ? nullptr : mirror[kind - 1]);
         }
     }
@@ -896,7 +903,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     float qf[MG][8];
     uint32_t qq[MG][2];
     float qdd[MG];
-    query_registers<KVT, MG>(a, G, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
+    query_registers<KVT, MG>(a, H, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
 
     float m_s[MG], l_s[MG], o[MG][8];
 #pragma unroll
@@ -983,8 +990,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     __syncthreads();
     // ---- merge the 4 waves; store this range's partial (agent-coherent) ----
     const int ns = a.n_split;
-    float *part = a.part + (size_t)g * G * ns * (hd + 2);
-    for (int i = tid; i < G * hd; i += 256) {
+    float *part = a.part + (size_t)h0 * ns * (hd + 2);
+    for (int i = tid; i < H * hd; i += 256) {
         const int j = i / hd, d = i % hd;
         float M = -INFINITY;
 #pragma unroll
@@ -1009,14 +1016,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     wait_vmem();
     __syncthreads();
     if (tid == 0) {
-        int *cnt = a.counters + g * ATT_CNT_STRIDE;  // one 128-byte line per KV head: no contention between heads
+        int *cnt = a.counters + blockIdx.y * ATT_CNT_STRIDE;  // one 128-byte line per head slice: no contention between slices
         const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == ns - 1;
         if (old == ns - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    combine_group<HD, G>(a, g, qs_f, wo_s[0], wm_s[0]);
+    combine_group<HD, H>(a, h0, qs_f, wo_s[0], wm_s[0]);
 }
 
 // merge the ranges of one (token, head); undo the rotation; quantize to Q8_0
@@ -1115,17 +1122,30 @@ static void launch_split_g(const AttnArgs &a, int G, dim3 grid, hipStream_t st) 
     else hipLaunchKernelGGL((attn_split_kernel<KVT, SUB, 8>), grid, dim3(256), 0, st, a);
 }
 
+// Query heads per decode workgroup: groups of 6 or 8 are split in two slices, which
+// halves the registers and LDS per workgroup and doubles the workgroups per range
+// (the two slices read the same K/V rows; they sit n_split blocks apart, on the
+// same XCD when n_split is a multiple of 8, so the second read is an L2 hit).
+int decode_heads_per_wg(int G) { return (G == 6 || G == 8) ? G / 2 : G; }
+
 template <int KVT, int HD>
 static void launch_decode_g(const AttnArgs &a, const HeadPrepArgs &hp, int G, dim3 grid, hipStream_t st) {
+    const bool split = decode_heads_per_wg(G) != G;
     switch (G) {
-    case 1: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 1>), grid, dim3(256), 0, st, a, hp); break;
-    case 2: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 2>), grid, dim3(256), 0, st, a, hp); break;
-    case 3: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 3>), grid, dim3(256), 0, st, a, hp); break;
-    case 4: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 4>), grid, dim3(256), 0, st, a, hp); break;
-    case 5: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 5>), grid, dim3(256), 0, st, a, hp); break;
-    case 6: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 6>), grid, dim3(256), 0, st, a, hp); break;
-    case 7: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 7>), grid, dim3(256), 0, st, a, hp); break;
-    default: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 8>), grid, dim3(256), 0, st, a, hp); break;
+    case 1: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 1, 1>), grid, dim3(256), 0, st, a, hp); break;
+    case 2: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 2, 2>), grid, dim3(256), 0, st, a, hp); break;
+    case 3: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 3, 3>), grid, dim3(256), 0, st, a, hp); break;
+    case 4: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 4, 4>), grid, dim3(256), 0, st, a, hp); break;
+    case 5: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 5, 5>), grid, dim3(256), 0, st, a, hp); break;
+    case 6:
+        if (split) hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 6, 3>), grid, dim3(256), 0, st, a, hp);
+        else hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 6, 6>), grid, dim3(256), 0, st, a, hp);
+        break;
+    case 7: hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 7, 7>), grid, dim3(256), 0, st, a, hp); break;
+    default:
+        if (split) hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 8, 4>), grid, dim3(256), 0, st, a, hp);
+        else hipLaunchKernelGGL((attn_decode_kernel<KVT, HD, 8, 8>), grid, dim3(256), 0, st, a, hp);
+        break;
     }
 }
 
@@ -1185,7 +1205,8 @@ bool attention_fused_ok(const AttnArgs &a) {
 
 bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {
     if (!attention_fused_ok(a) || hp.n_tok != 1) return false;
-    const dim3 grid(a.n_split, a.n_kv, 1);
+    const int G = a.n_head / a.n_kv;
+    const dim3 grid(a.n_split, a.n_kv * (G / decode_heads_per_wg(G)), 1);
     switch (a.kv_type) {
     case 0: launch_decode_kvt<0>(a, hp, grid, st); break;
     case 1: launch_decode_kvt<1>(a, hp, grid, st); break;

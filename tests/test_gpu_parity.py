@@ -403,6 +403,42 @@ def test_prompt_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv
                         f"hd {hd} G {G} layer {layer} token {p} head {hq}: {err}"
 
 
+@pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
+def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv):
+    """Single-token attention (the fused launch: prep, append, context ranges,
+    range merge; groups of 6 and 8 query heads split in two workgroups) at
+    positions 296..299 against a float64 evaluation of cpu.rs:550-634 on the
+    prepared queries and the f16 cache rows, to the f32 bound of the prompt
+    test above."""
+    def mut(s):
+        s.head_dim, s.n_head, s.n_head_kv, s.rope_dim = hd, nh, nkv, hd
+    n_ctx = 320
+    spec, g, _ = _pair(oracle, "llama", Q8_0, 0, n_ctx=n_ctx, max_batch=64, mutate=mut)
+    G, qd = nh // nkv, nh * hd
+    toks = [(i * 53 + 11) % spec.n_vocab for i in range(300)]
+    for pos in range(0, 296, 64):
+        g.forward(toks[pos:min(pos + 64, 296)], pos)
+    g.set_capture(True)
+    for p in range(296, 300):
+        g.forward([toks[p]], p)
+        for layer in range(spec.n_layer):
+            q = g.capture(layer, 3, qd).reshape(nh, hd).astype(np.float64)
+            att = g.capture(layer, 2, qd).reshape(nh, hd)
+            kr, _ = g.kv_layer(layer, 0, nkv, n_ctx)
+            vr, _ = g.kv_layer(layer, 1, nkv, n_ctx)
+            K = kr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+            V = vr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+            for hq in range(nh):
+                kv = hq // G
+                s = K[kv, :p + 1] @ q[hq]
+                w = np.exp(s - s.max())
+                ref = (w / w.sum()) @ V[kv, :p + 1]
+                err = np.max(np.abs(att[hq] - ref))
+                vmax = np.max(np.abs(V[kv, :p + 1]))
+                assert err <= (8 * 2.0 ** -24 * np.max(np.abs(s)) + 5e-6) * vmax + 1e-6, \
+                    f"hd {hd} G {G} layer {layer} token {p} head {hq}: {err}"
+
+
 @pytest.mark.parametrize("kv", [0, 1, 2])
 def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
     """The cache rows the GPU writes equal the reference encoders applied to the
