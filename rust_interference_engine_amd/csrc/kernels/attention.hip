@@ -754,8 +754,11 @@ __device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts,
 #pragma unroll
         for (int k = 0; k < ATT_MAX_SPLIT / 64; k++) {
             const int s = lane + 64 * k;
+            // zero past ns: the sums below run over whole batches of CB ranges
+            // without a branch per range (the clamped partials they then read are
+            // finite, so each such term adds an exact zero)
             const float w = (s < ns && lv[k] > 0.0f) ? exp2_hw(mv[k] - m) : 0.0f;
-            if (s < ns) wts[j * ATT_MAX_SPLIT + s] = w;
+            wts[j * ATT_MAX_SPLIT + s] = w;
             L += s < ns ? lv[k] * w : 0.0f;
         }
         L = wave_sum(L, 64);
@@ -773,14 +776,12 @@ __device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts,
         for (int b = 0; b < CB; b++) v[b] = r < NPF ? pre[r < NPF ? r : 0][b] : ld_coh(src + (size_t)min(b, ns - 1) * prow);
         float acc = 0.0f;
 #pragma unroll
-        for (int b = 0; b < CB; b++)
-            if (b < ns) acc = fmaf(v[b], w[b], acc);
-        for (int s0 = CB; s0 < ns; s0 += CB) {
+        for (int b = 0; b < CB; b++) acc = fmaf(v[b], w[b], acc);
+        for (int s0 = CB; s0 < ns; s0 += CB) {  // ns is a power of two: whole batches
 #pragma unroll
-            for (int b = 0; b < CB; b++) v[b] = ld_coh(src + (size_t)min(s0 + b, ns - 1) * prow);
+            for (int b = 0; b < CB; b++) v[b] = ld_coh(src + (size_t)(s0 + b) * prow);
 #pragma unroll
-            for (int b = 0; b < CB; b++)
-                if (s0 + b < ns) acc = fmaf(v[b], w[s0 + b], acc);
+            for (int b = 0; b < CB; b++) acc = fmaf(v[b], w[s0 + b], acc);
         }
         if (tid + 256 * r < n_out) o_s[i] = acc * (1.0f / Ls[j]);
     }
@@ -805,20 +806,24 @@ __device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts,
     const size_t base = (size_t)h0 * hd;
     for (int i = tid; i < G * hd; i += 256) a.att[base + i] = o_s[i];
     if (a.att_fmt == ACT_Q8_0) {  // hd % 32 == 0: the group's values are whole blocks
-        const int hw = tid >> 5, j = tid & 31;
-        for (int bi = hw; bi < G * hd / 32; bi += 8) {
-            const float y = o_s[bi * 32 + j];
-            float amax = fabsf(y);
-            amax = xmax_f<32>(amax);
+        // 16 lanes per block, values j and j + 16 in lane j (max and integer sums
+        // are exact in any order, so the codes are those of the reference's quantizer)
+        const int hb = tid >> 4, j = tid & 15;
+        for (int bi = hb; bi < G * hd / 32; bi += 16) {
+            const float y0 = o_s[bi * 32 + j], y1 = o_s[bi * 32 + j + 16];
+            float amax = fmaxf(fabsf(y0), fabsf(y1));
+            amax = xmax_f<16>(amax);
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            const int q = (int)rintf(y * id);
-            const int qc = q < -127 ? -127 : (q > 127 ? 127 : q);
-            int su = q, scl = qc;
-            su = xsum_i<32>(su);
-            scl = xsum_i<32>(scl);
+            const int q0 = (int)rintf(y0 * id), q1 = (int)rintf(y1 * id);
+            const int c0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+            const int c1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+            int su = q0 + q1, scl = c0 + c1;
+            su = xsum_i<16>(su);
+            scl = xsum_i<16>(scl);
             const size_t e = base + bi * 32 + j;
-            a.att_q.qs[e] = (int8_t)qc;
+            a.att_q.qs[e] = (int8_t)c0;
+            a.att_q.qs[e + 16] = (int8_t)c1;
             if (j == 0) {
                 const size_t blk = e / 32;
                 a.att_q.d[blk] = d;
@@ -1199,8 +1204,9 @@ void launch_attention(const AttnArgs &a, hipStream_t st) {
 
 bool attention_fused_ok(const AttnArgs &a) {
     const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
+    // the range merge reads whole batches of 16 ranges past the first: n_split a power of two
     return a.n_tok == 1 && a.counters && (a.hd == 64 || a.hd == 128 || a.hd == 256) && G >= 1 && G <= 8 && a.n_head == G * a.n_kv &&
-           a.n_split <= ATT_MAX_SPLIT;
+           a.n_split >= 1 && a.n_split <= ATT_MAX_SPLIT && (a.n_split & (a.n_split - 1)) == 0;
 }
 
 bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {
