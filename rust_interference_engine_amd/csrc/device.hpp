@@ -57,6 +57,26 @@ __device__ __forceinline__ int xor_i(int v) {
 template <int OFF>
 __device__ __forceinline__ float xor_f(float v) { return __int_as_float(xor_i<OFF>(__float_as_int(v))); }
 
+// Both values of the lane pair {l & ~OFF, l | OFF} (OFF = 16 or 32), in both lanes of
+// the pair: lo = v[l & ~OFF], hi = v[l | OFF].  One v_permlane16_swap /
+// v_permlane32_swap (VALU, no LDS).  A symmetric merge written as f(lo, hi) gives
+// both lanes the same bits, which are those of f(own, other) up to the order of
+// commutative operations.
+template <int OFF>
+__device__ __forceinline__ void pair_f(float v, float &lo, float &hi) {
+    static_assert(OFF == 16 || OFF == 32, "lane offset");
+    const unsigned iv = __float_as_uint(v);
+    if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    }
+}
+
 // f(std::integral_constant<int, O>) for O = FROM, FROM/2, …, TO, or (xor_up) for
 // O = FROM, 2·FROM, …, TO: lane-offset loops whose offsets are template arguments.
 template <int FROM, int TO, class F>

@@ -969,14 +969,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
         constexpr int off = decltype(oc)::value;
 #pragma unroll
         for (int j = 0; j < MG; j++) {
-            const float mo = xor_f<off>(m_s[j]), lo = xor_f<off>(l_s[j]);
-            const float M = fmaxf(m_s[j], mo);
-            const bool any = M != -INFINITY;
-            const float a1 = any ? exp2_hw(m_s[j] - M) : 0.0f, a2 = any ? exp2_hw(mo - M) : 0.0f;
-            l_s[j] = l_s[j] * a1 + lo * a2;
+            if constexpr (off >= 16) {  // lane pairs by permlane swaps: f(lower lane's slot, upper lane's slot)
+                float m0, m1, l0, l1;
+                pair_f<off>(m_s[j], m0, m1);
+                pair_f<off>(l_s[j], l0, l1);
+                const float M = fmaxf(m0, m1);
+                const bool any = M != -INFINITY;
+                const float a0 = any ? exp2_hw(m0 - M) : 0.0f, a1 = any ? exp2_hw(m1 - M) : 0.0f;
+                l_s[j] = l0 * a0 + l1 * a1;
 #pragma unroll
-            for (int i = 0; i < 8; i++) o[j][i] = o[j][i] * a1 + xor_f<off>(o[j][i]) * a2;
-            m_s[j] = M;
+                for (int i = 0; i < 8; i++) {
+                    float o0, o1;
+                    pair_f<off>(o[j][i], o0, o1);
+                    o[j][i] = o0 * a0 + o1 * a1;
+                }
+                m_s[j] = M;
+            } else {
+                const float mo = xor_f<off>(m_s[j]), lo = xor_f<off>(l_s[j]);
+                const float M = fmaxf(m_s[j], mo);
+                const bool any = M != -INFINITY;
+                const float a1 = any ? exp2_hw(m_s[j] - M) : 0.0f, a2 = any ? exp2_hw(mo - M) : 0.0f;
+                l_s[j] = l_s[j] * a1 + lo * a2;
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[j][i] = o[j][i] * a1 + xor_f<off>(o[j][i]) * a2;
+                m_s[j] = M;
+            }
         }
     });
     if (lane < SUB && cact) {
