@@ -568,21 +568,36 @@ void HipBackend::ffn_moe(const DevLayer &L, int n) {
     const ModelConfig &c = m_.cfg;
     const int E = (int)c.n_embd, ne = (int)c.n_expert, k = (int)L.n_used, ff = (int)L.ff;
     const bool shared = L.sh_gate.data != nullptr;
-    const DevWeight *ws[4] = {&L.router, &L.gate, &L.up, shared ? &L.sh_gate : nullptr};
-    prepare(d_x_, L.ffn_norm, n, E, ws, 4, true);  // f32 rows for the router, gathers and the shared gate
+    // One token without a shared expert: the router GEMV and the experts' gate/up
+    // normalize x in their prologues (the same values as the standalone norm's
+    // rows and codes), so neither the norm launch nor the row copy runs.
+    const bool self_norm = n == 1 && !capture_ && !shared && L.ffn_norm && L.gate.ty == L.up.ty &&
+                           (gemv_norm_f32_ok(L.router.ty, E) || gemv_norm_ok(L.router.ty, E)) && gemv_norm_ok(L.gate.ty, E);
+    // the router's f32 rows follow the kernel prepare() would have made them with
+    const NormIn nin{d_x_, L.ffn_norm, c.rms_eps, act_format(L.gate.ty) == ACT_Q8_0 ? 1 : 0};
+    if (!self_norm) {
+        const DevWeight *ws[4] = {&L.router, &L.gate, &L.up, shared ? &L.sh_gate : nullptr};
+        prepare(d_x_, L.ffn_norm, n, E, ws, 4, true);  // f32 rows for the router, gathers and the shared gate
+    }
     mark("rmsnorm_quant");
     GemvSeg rs{L.router, d_router_, ne, EPI_STORE};
-    matmul(&rs, 1, n, E);
+    if (self_norm) {
+        if (!launch_gemv(&rs, 1, act_format(L.router.ty) == ACT_Q8K ? actk_ : act0_, d_xn_, 1, E, st_, &nin))
+            throw rt_err("normalizing router GEMV launch failed");
+    } else {
+        matmul(&rs, 1, n, E);
+    }
     launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
     check_launch("moe route");
     mark("moe_route");
-    RIE_HIP_CHECK(hipMemcpyAsync(d_moe_xn_, d_xn_, (size_t)n * E * 4, hipMemcpyDeviceToDevice, st_));
+    if (!self_norm) RIE_HIP_CHECK(hipMemcpyAsync(d_moe_xn_, d_xn_, (size_t)n * E * 4, hipMemcpyDeviceToDevice, st_));
     if (n == 1) {
         const ActQ8 &ax = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
         const int dfmt = act_format(L.down.ty);
+        const NormIn *gn = self_norm ? &nin : nullptr;
         bool hq = dfmt == ACT_Q8_0 && ff % 32 == 0 &&
-                  launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, &act_h_, st_);
-        if (!hq && !launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, nullptr, st_))
+                  launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, &act_h_, st_, gn);
+        if (!hq && !launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, nullptr, st_, gn))
             throw Error{E_UNSUPPORTED, "unsupported: routed expert weights"};
         mark("moe_gate_up_glu");
         if (!hq && dfmt != ACT_F32) launch_quant_only(d_h_, ff, k, ff, dfmt, dfmt == ACT_Q8K ? actk_ : act0_, st_);

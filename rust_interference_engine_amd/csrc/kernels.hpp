@@ -29,8 +29,15 @@ struct NormIn {
     const float *x;   // residual row [K]
     const float *w;   // norm weight [K]
     float eps;
+    // F32 weights only: the order of the scale's partial sums, that of the
+    // standalone kernel whose rows the prologue replaces: 1 = q8_0_rows_kernel
+    // (thread τ: values 16τ..16τ+15 of each 4096-value pass), 0 = rms_scale_wg
+    // (float4 at 4τ + 1024k)
+    int order16;
 };
 bool gemv_norm_ok(int ty, size_t K);
+// F32 weights with nin: the activation is RMSNorm(x)·w in f32, equal to the standalone norm's rows
+bool gemv_norm_f32_ok(int ty, size_t K);
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
                  const NormIn *nin = nullptr);
 // h = act(gate·x) ⊙ (up·x) for gated feed-forward blocks (gelu selects GELU-tanh).
@@ -111,8 +118,10 @@ void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *
 // when act_per_slot); the GLU variant writes h [n_slots][ff].
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
                          const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st);
+// With nin (gemv_norm_ok types) every workgroup forms the activation from RMSNorm(x)·w itself.
 bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
-                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st);
+                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st,
+                             const NormIn *nin = nullptr);
 
 // ---- gemm_kq.hip (prefill, Q4_K × Q8_K on int8 MFMA; reached through gemm.hip) ----
 bool gemm_kq_supported(int ty, size_t K);

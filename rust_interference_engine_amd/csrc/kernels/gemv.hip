@@ -384,6 +384,43 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             have_act = true;
         }
     }
+    if constexpr (TY == T_F32) {
+        if (p.nin.x) {
+            // The activation is RMSNorm(x)·w in f32, bit for bit the rows of the
+            // standalone kernel it replaces: the scale from that kernel's partial
+            // sums (the first 256 threads; q8_0_rows_kernel's 16 consecutive values
+            // per thread and 4096-value pass, or rms_scale_wg's float4 at
+            // 4τ + 1024k), then (x·scale)·w per value.
+            __shared__ float s_red[4];
+            const int K = p.K;
+            float ss = 0.0f;
+            if (tid < 256) {
+                const int step = p.nin.order16 ? 4096 : 1024;
+                for (int i0 = p.nin.order16 ? 16 * tid : 4 * tid; i0 < K; i0 += step)
+                    for (int k = 0; k < (p.nin.order16 ? 4 : 1); k++) {
+                        const float4 v = *(const float4 *)(p.nin.x + i0 + 4 * k);
+                        ss = fmaf(v.x, v.x, ss);
+                        ss = fmaf(v.y, v.y, ss);
+                        ss = fmaf(v.z, v.z, ss);
+                        ss = fmaf(v.w, v.w, ss);
+                    }
+            }
+            ss = wave_sum(ss, 64);
+            if ((tid & 63) == 0 && tid < 256) s_red[tid >> 6] = ss;
+            __syncthreads();
+            const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const float4 *xp = (const float4 *)(p.nin.x + 8 * uu[k]), *wp = (const float4 *)(p.nin.w + 8 * uu[k]);
+                const float4 x0 = xp[0], x1 = xp[1], w0 = wp[0], w1 = wp[1];
+                a[k].f[0] = x0.x * scale * w0.x; a[k].f[1] = x0.y * scale * w0.y;
+                a[k].f[2] = x0.z * scale * w0.z; a[k].f[3] = x0.w * scale * w0.w;
+                a[k].f[4] = x1.x * scale * w1.x; a[k].f[5] = x1.y * scale * w1.y;
+                a[k].f[6] = x1.z * scale * w1.z; a[k].f[7] = x1.w * scale * w1.w;
+            }
+            have_act = true;
+        }
+    }
     if (!have_act) {
 #pragma unroll
         for (int k = 0; k < UPL; k++)
@@ -638,12 +675,14 @@ bool gemv_norm_ok(int ty, size_t K) {
     return false;
 }
 
+bool gemv_norm_f32_ok(int ty, size_t K) { return ty == T_F32 && K % 16 == 0 && K >= 16; }
+
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
                  const NormIn *nin) {
     if (n_tok < 1) return false;
     if (nin && (n_tok != 1 || !nin->x || !nin->w)) return false;
     for (int s = 0; s < nseg; s++)
-        if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K)) return false;
+        if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K) && !gemv_norm_f32_ok(segs[s].w.ty, (size_t)K)) return false;
     // segments of one launch must share a weight type; split otherwise
     int i = 0;
     while (i < nseg) {
@@ -701,7 +740,8 @@ bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel
 }
 
 bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
-                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st) {
+                             const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st, const NormIn *nin) {
+    if (nin && (!nin->x || !nin->w || !gemv_norm_ok(gate.ty, (size_t)K))) return false;
     if (gate.ty != up.ty || !gemv_supported(gate.ty, (size_t)K) || gate.cols != (size_t)K || up.cols != (size_t)K ||
         gate.rows != up.rows || gate.rows % (size_t)ff || !gate.data || !up.data || !h || !sel || n_slots < 1 ||
         !operands_ok(gate.ty, act, act_f32))
@@ -716,6 +756,7 @@ bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff,
     d.actf = act_f32;
     d.glu = gelu ? 2 : 1;
     if (hq) d.hq = *hq;
+    if (nin) d.nin = *nin;
     d.xsel = sel;
     d.slot_rows = ff;
     return dispatch_dec(gate.ty, d, st);
