@@ -327,13 +327,14 @@ def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
         assert err < tol, f"{arch} {ty}: decode token {t}: {err}"
 
 
-@pytest.mark.parametrize("ty", [Q4_K, Q4_0])
-def test_moe_decode_prologues_equal_standalone_norm(oracle, cuda, ty):
-    """One-token MoE decode normalizes x inside the router GEMV (f32 rows) and
-    inside the experts' gate/up (activation codes); capture mode runs the
-    standalone RMSNorm launches instead.  Decoding the same tokens at the same
-    positions both ways gives bitwise equal logits."""
-    spec, g, _ = _pair(oracle, "qwen3moe", ty, 0, n_ctx=64, max_batch=16)
+@pytest.mark.parametrize("arch,ty", [("qwen3moe", Q4_K), ("qwen3moe", Q4_0), ("llama", Q4_0), ("llama", Q4_K)])
+def test_decode_prologues_equal_standalone_norm(oracle, cuda, arch, ty):
+    """One-token decode normalizes x inside the GEMVs that read it: Q/K/V and
+    gate/up (activation codes), and for MoE layers the router (f32 rows) and the
+    experts' gate/up; capture mode runs the standalone RMSNorm launches instead.
+    Decoding the same tokens at the same positions both ways gives bitwise
+    equal logits."""
+    spec, g, _ = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16)
     toks = [(i * 41 + 7) % spec.n_vocab for i in range(20)]
     g.forward(toks[:16], 0)
     fused = [np.array(g.forward([toks[t]], t)) for t in range(16, 20)]
@@ -341,7 +342,7 @@ def test_moe_decode_prologues_equal_standalone_norm(oracle, cuda, ty):
     for i, t in enumerate(range(16, 20)):
         plain = np.array(g.forward([toks[t]], t))
         assert np.array_equal(fused[i].view(np.uint32), plain.view(np.uint32)), \
-            f"{ty}: token {t}: max diff {np.max(np.abs(fused[i] - plain))}"
+            f"{arch} {ty}: token {t}: max diff {np.max(np.abs(fused[i] - plain))}"
 
 
 ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32, query groups 1..8
