@@ -481,9 +481,10 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
         // ---- feed-forward block ----
         const bool fdirect = !L.post_ffn_norm && c.residual_scale == 1.0f;
         if (L.moe) {
-            ffn_moe(L, n);
-            if (L.post_ffn_norm) launch_rmsnorm(d_o_, E, L.post_ffn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);
-            launch_add_inplace(d_x_, d_o_, (size_t)n * E, c.residual_scale, st_);
+            if (!ffn_moe(L, n, fdirect)) {
+                if (L.post_ffn_norm) launch_rmsnorm(d_o_, E, L.post_ffn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);
+                launch_add_inplace(d_x_, d_o_, (size_t)n * E, c.residual_scale, st_);
+            }
         } else {
             ffn_dense(L, n, fdirect ? d_x_ : d_o_, fdirect ? EPI_ADD : EPI_STORE);
             if (capture_ && !in_capture_) {
@@ -564,7 +565,10 @@ void HipBackend::expert_ffn(const DevWeight &g, const DevWeight &u, const DevWei
 // d_o_, plus the optionally gated shared expert.  One token: everything stays on
 // the device (graph replay); prompt batches read the routing back and run each
 // selected expert once over its gathered tokens.
-void HipBackend::ffn_moe(const DevLayer &L, int n) {
+// direct: the caller's residual add is a plain x += y (no post-norm, scale 1); a
+// single token without a shared expert then combines straight into x, and the
+// return value says so (x + y is what the add kernel computes at scale 1).
+bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
     const ModelConfig &c = m_.cfg;
     const int E = (int)c.n_embd, ne = (int)c.n_expert, k = (int)L.n_used, ff = (int)L.ff;
     const bool shared = L.sh_gate.data != nullptr;
@@ -605,6 +609,12 @@ void HipBackend::ffn_moe(const DevLayer &L, int n) {
         if (!launch_gemv_experts(L.down, E, d_moe_sel_, k, ah, d_h_, true, ff, d_moe_y_, st_))
             throw Error{E_UNSUPPORTED, "unsupported: routed expert down weights"};
         mark("moe_down");
+        if (direct && !shared && !capture_) {  // capture keeps the two-step form (a bitwise check of this one)
+            launch_moe_combine(d_moe_y_, d_moe_w_, 1, k, E, d_x_, EPI_ADD, st_);
+            check_launch("moe");
+            mark("moe_combine");
+            return true;
+        }
         launch_moe_combine(d_moe_y_, d_moe_w_, 1, k, E, d_o_, EPI_STORE, st_);
     } else {
         std::vector<int> sel((size_t)n * k);
@@ -650,6 +660,7 @@ void HipBackend::ffn_moe(const DevLayer &L, int n) {
     }
     check_launch("moe");
     mark("moe_combine");
+    return false;
 }
 
 void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_logits, float *logits, size_t logits_len) {

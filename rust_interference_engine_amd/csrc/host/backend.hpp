@@ -91,7 +91,8 @@ class HipBackend {
     void prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32);
     void matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0 = nullptr);
     void ffn_dense(const DevLayer &L, int n, float *out_resid, int epi);
-    void ffn_moe(const DevLayer &L, int n);  // writes the block's output to d_o_
+    // writes the block's output to d_o_, or (true returned) adds it to d_x_ itself
+    bool ffn_moe(const DevLayer &L, int n, bool direct);
     void expert_ffn(const DevWeight &g, const DevWeight &u, const DevWeight &dn, const float *x, int m, float *y);
     void head(int first, int m);
     void check_launch(const char *what);
