@@ -705,13 +705,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 }
 
 // ---- single token (decode) ----------------------------------------------------------
-// One launch per layer, grid (n_split, n_kv).  The workgroup prepares its group's
-// query heads itself (bias, RMSNorm, RoPE, scale); the workgroup whose range holds
+// One launch per layer, grid (n_split, n_kv · slices per group).  The workgroup
+// prepares its query heads itself (bias, RMSNorm, RoPE, scale); the workgroup whose range holds
 // the new position also prepares, encodes and appends that position's K and V row
 // and uses its LDS copy of the encoded row.  Each SUB-lane position slot keeps its
 // own online softmax state in registers (no LDS or barrier inside the tile loop);
 // the slots are merged by shuffles within the wave and through LDS across the 4
-// waves.  The last workgroup of each KV head to finish merges the ranges, undoes
+// waves.  The last workgroup of each head slice to finish merges the ranges, undoes
 // the Turbo4 rotation and writes att (f32 and Q8_0).
 
 // Merge of the n_split range partials of query heads h0 .. h0 + G - 1 by the last
@@ -1148,7 +1148,7 @@ static void launch_split_g(const AttnArgs &a, int G, dim3 grid, hipStream_t st) 
 // halves the registers and LDS per workgroup and doubles the workgroups per range
 // (the two slices read the same K/V rows; they sit n_split blocks apart, on the
 // same XCD when n_split is a multiple of 8, so the second read is an L2 hit).
-int decode_heads_per_wg(int G) { return (G == 6 || G == 8) ? G / 2 : G; }
+static int decode_heads_per_wg(int G) { return (G == 6 || G == 8) ? G / 2 : G; }
 
 template <int KVT, int HD>
 static void launch_decode_g(const AttnArgs &a, const HeadPrepArgs &hp, int G, dim3 grid, hipStream_t st) {
