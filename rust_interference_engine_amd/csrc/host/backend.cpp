@@ -604,9 +604,14 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
         if (!hq && !launch_gemv_glu_experts(L.gate, L.up, ff, d_moe_sel_, k, ax, d_xn_, E, d_h_, c.gelu, nullptr, st_, gn))
             throw Error{E_UNSUPPORTED, "unsupported: routed expert weights"};
         mark("moe_gate_up_glu");
-        if (!hq && dfmt != ACT_F32) launch_quant_only(d_h_, ff, k, ff, dfmt, dfmt == ACT_Q8K ? actk_ : act0_, st_);
+        // Q8_K down weights: the down GEMV quantizes its expert's hidden row in its
+        // prologue (the standalone quantizer's codes) instead of a quantizer launch;
+        // capture mode keeps the launch (a bitwise check of this form)
+        const bool hpro = !hq && !capture_ && dfmt == ACT_Q8K && gemv_norm_ok(L.down.ty, ff);
+        if (!hq && dfmt != ACT_F32 && !hpro) launch_quant_only(d_h_, ff, k, ff, dfmt, dfmt == ACT_Q8K ? actk_ : act0_, st_);
         const ActQ8 &ah = hq ? act_h_ : (dfmt == ACT_Q8K ? actk_ : act0_);
-        if (!launch_gemv_experts(L.down, E, d_moe_sel_, k, ah, d_h_, true, ff, d_moe_y_, st_))
+        const NormIn hn{d_h_, nullptr, 0.0f, 0};
+        if (!launch_gemv_experts(L.down, E, d_moe_sel_, k, ah, d_h_, true, ff, d_moe_y_, st_, hpro ? &hn : nullptr))
             throw Error{E_UNSUPPORTED, "unsupported: routed expert down weights"};
         mark("moe_down");
         if (direct && !shared && !capture_) {  // capture keeps the two-step form (a bitwise check of this one)

@@ -116,8 +116,11 @@ void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *
 // Routed experts of one token (stacked expert tensors, expert ids on the device):
 // out rows [j·slot_rows, (j+1)·slot_rows) = expert sel[j]'s rows · act (act row j
 // when act_per_slot); the GLU variant writes h [n_slots][ff].
+// With nin (Q8_K weight types): every workgroup quantizes its activation row from
+// nin->x itself (normalized first when nin->w is given).
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
-                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st);
+                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st,
+                         const NormIn *nin = nullptr);
 // With nin (gemv_norm_ok types) every workgroup forms the activation from RMSNorm(x)·w itself.
 bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff, const int *sel, int n_slots, const ActQ8 &act,
                              const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st,

@@ -308,14 +308,19 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             // largest |y| (DPP within the 16-lane row, the lower index winning
             // ties), iscale = −127/max, round-half-away codes, the thread's 16-value
             // sum, d = 1/iscale.  Every code equals the standalone kernel's.
+            // Without a norm weight the prologue only quantizes (y = x·1·1 = x,
+            // exactly), reading the workgroup's slot row when activations are per
+            // slot (an expert's hidden).
             __shared__ __align__(16) int8_t s_q[4096];
             __shared__ float s_d[16], s_red[4];
             __shared__ __align__(16) int16_t s_bs[256];
             const int K = p.K;
+            const bool norm = p.nin.w != nullptr;
+            const float *xr = p.nin.x + ((p.xsel && p.act_per_slot) ? (size_t)slot * K : 0);
             float ss = 0.0f;
-            if (tid < 256)
+            if (norm && tid < 256)
                 for (int i = tid * 4; i < K; i += 1024) {
-                    const float4 v = *(const float4 *)(p.nin.x + i);
+                    const float4 v = *(const float4 *)(xr + i);
                     ss = fmaf(v.x, v.x, ss);
                     ss = fmaf(v.y, v.y, ss);
                     ss = fmaf(v.z, v.z, ss);
@@ -324,12 +329,13 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             ss = wave_sum(ss, 64);
             if ((tid & 63) == 0 && tid < 256) s_red[tid >> 6] = ss;
             __syncthreads();
-            const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+            const float scale = norm ? 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps) : 1.0f;
             if (tid < (K >> 4)) {  // whole 16-lane rows
                 float y[16];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float4 xv = ((const float4 *)(p.nin.x + 16 * tid))[i], gv = ((const float4 *)(p.nin.w + 16 * tid))[i];
+                    const float4 xv = ((const float4 *)(xr + 16 * tid))[i];
+                    const float4 gv = norm ? ((const float4 *)(p.nin.w + 16 * tid))[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
                     y[4 * i] = xv.x * scale * gv.x;
                     y[4 * i + 1] = xv.y * scale * gv.y;
                     y[4 * i + 2] = xv.z * scale * gv.z;
@@ -722,7 +728,9 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
 }
 
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
-                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st) {
+                         const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st, const NormIn *nin) {
+    // with nin: the K-quant prologue quantizes (and with nin->w normalizes) the activation itself
+    if (nin && (!nin->x || act_format(stacked.ty) != ACT_Q8K || !gemv_norm_ok(stacked.ty, (size_t)K))) return false;
     if (!gemv_supported(stacked.ty, (size_t)K) || stacked.cols != (size_t)K || !stacked.data || !out || !sel || n_slots < 1 ||
         slot_rows < 1 || stacked.rows % (size_t)slot_rows || !operands_ok(stacked.ty, act, act_f32))
         return false;
@@ -736,6 +744,7 @@ bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel
     d.xsel = sel;
     d.slot_rows = slot_rows;
     d.act_per_slot = act_per_slot;
+    if (nin) d.nin = *nin;
     return dispatch_dec(stacked.ty, d, st);
 }
 
