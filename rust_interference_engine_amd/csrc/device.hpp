@@ -12,17 +12,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 
 // Weight-stream loads.  Plain loads: on gfx950 the nontemporal form measured
-// about 35% slower for the decode GEMVs (RIE_WEIGHT_NT=1 selects it).
-#ifndef RIE_WEIGHT_NT
-#define RIE_WEIGHT_NT 0
-#endif
+// about 35% slower for the decode GEMVs.
 template <class T>
 __device__ __forceinline__ T wload(const T *p) {
-#if RIE_WEIGHT_NT
-    return __builtin_nontemporal_load(p);
-#else
     return *p;
-#endif
 }
 __device__ __forceinline__ u32x4 ld_w16(const void *p) { return wload((const u32x4 *)p); }
 __device__ __forceinline__ f32x4 ld_w16f(const void *p) { return wload((const f32x4 *)p); }

@@ -115,6 +115,10 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
             D.ff = c.n_ff_exp;
             D.norm_topk = L.norm_topk;
             D.unit_weights = L.unit_weights;
+            // the shared expert's hidden goes through the same scratch as the routed ones
+            // (cpu.rs:134-140 sizes its buffers over dense, expert and shared-expert widths)
+            if (D.sh_gate.data) ff_max_ = std::max(ff_max_, D.sh_gate.rows);
+            n_used_max_ = std::max(n_used_max_, D.n_used);
         } else {
             D.ff = L.gate.rows;
         }
@@ -197,16 +201,18 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     d_kcap_ = dalloc<float>(allocs_, mb * kvd);
     d_att_ = dalloc<float>(allocs_, mb * qd);
     d_o_ = dalloc<float>(allocs_, mb * E);
-    d_h_ = dalloc<float>(allocs_, mb * ff_max_ * (c.n_expert ? c.n_expert_used : 1));
+    // routed experts per token as the layers run them (clamped to [1, n_expert], model/mod.rs:176)
+    const size_t nu = std::max<size_t>(n_used_max_, 1);
+    d_h_ = dalloc<float>(allocs_, mb * ff_max_ * nu);
     d_logits_ = dalloc<float>(allocs_, mb * c.n_vocab);
-    const size_t kq = mb * kmax_ * (c.n_expert ? c.n_expert_used : 1);
+    const size_t kq = mb * kmax_ * nu;
     act0_.qs = dalloc<int8_t>(allocs_, kq);
     act0_.d = dalloc<float>(allocs_, kq / 32);
     act0_.s = dalloc<float>(allocs_, kq / 32);
     act0_.isum = dalloc<int32_t>(allocs_, kq / 32);
     // Q8_0 of the single-token FFN hidden, written by the gate/up kernel while
     // it still reads act0_
-    const size_t hrows = c.n_expert ? c.n_expert_used : 1;  // routed experts of one token
+    const size_t hrows = nu;  // routed experts of one token
     act_h_.qs = dalloc<int8_t>(allocs_, hrows * ff_max_);
     act_h_.d = dalloc<float>(allocs_, hrows * ff_max_ / 32 + 1);
     act_h_.s = dalloc<float>(allocs_, hrows * ff_max_ / 32 + 1);
@@ -221,14 +227,14 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
     if (c.n_expert) {
         d_router_ = dalloc<float>(allocs_, mb * c.n_expert);
-        d_moe_w_ = dalloc<float>(allocs_, mb * c.n_expert_used);
-        d_moe_sel_ = dalloc<int>(allocs_, mb * c.n_expert_used);
-        d_moe_y_ = dalloc<float>(allocs_, mb * c.n_expert_used * E);
+        d_moe_w_ = dalloc<float>(allocs_, mb * nu);
+        d_moe_sel_ = dalloc<int>(allocs_, mb * nu);
+        d_moe_y_ = dalloc<float>(allocs_, mb * nu * E);
         d_moe_xn_ = dalloc<float>(allocs_, mb * E);
         d_moe_xg_ = dalloc<float>(allocs_, mb * E);
         d_moe_yg_ = dalloc<float>(allocs_, mb * E);
-        d_moe_rows_ = dalloc<int>(allocs_, mb * c.n_expert_used);
-        d_moe_rw_ = dalloc<float>(allocs_, mb * c.n_expert_used);
+        d_moe_rows_ = dalloc<int>(allocs_, mb * nu);
+        d_moe_rw_ = dalloc<float>(allocs_, mb * nu);
     }
     cap_.resize(7);
     RIE_HIP_CHECK(hipDeviceSynchronize());

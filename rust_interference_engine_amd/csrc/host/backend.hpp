@@ -129,6 +129,7 @@ class HipBackend {
     ActQ8 act0_, actk_;  // Q8_0 and Q8_K batches
     ActQ8 act_h_;        // Q8_0 of the single-token FFN hidden
     size_t kmax_ = 0, ff_max_ = 0, part_floats_ = 0;
+    size_t n_used_max_ = 0;  // largest clamped routed-expert count of any MoE layer
     // MoE scratch
     float *d_router_ = nullptr, *d_moe_w_ = nullptr, *d_moe_y_ = nullptr;
     float *d_moe_xn_ = nullptr, *d_moe_xg_ = nullptr, *d_moe_yg_ = nullptr, *d_moe_rw_ = nullptr;

@@ -65,10 +65,7 @@ __device__ __forceinline__ void load_wunit(const uint8_t *row, int b, WUnit<TY> 
 // the workgroup stages the activation codes and scales and the weight codes
 // (nibbles kept packed, 16 B/block for Q4_0) and scales in LDS; the next
 // stage's global loads are in flight while the current stage is multiplied.
-#ifndef RIE_GEMM_KC
-#define RIE_GEMM_KC 4  // 32-value blocks per LDS stage
-#endif
-constexpr int G_BM = 64, G_KC = RIE_GEMM_KC;
+constexpr int G_BM = 64, G_KC = 4;  // G_KC: 32-value blocks per LDS stage
 constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, padded)
 
 template <int TY>

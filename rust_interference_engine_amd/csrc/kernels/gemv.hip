@@ -146,16 +146,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvP p) {
     }
 }
 
-// rows whose loads a wave keeps in flight together (register budget ≈ R × unit bytes)
-#ifndef RIE_DEC_ROWS_SMALL
-#define RIE_DEC_ROWS_SMALL 4  // units of ≤ 48 bytes: Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q4_K, F16, BF16
-#endif
-#ifndef RIE_DEC_ROWS_LARGE
-#define RIE_DEC_ROWS_LARGE 2  // Q8_0, Q3_K, Q5_K, Q6_K, F32
-#endif
+// rows whose loads a wave keeps in flight together (register budget ≈ R × unit
+// bytes): 4 for units of ≤ 48 bytes (Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q4_K, F16,
+// BF16), 2 for Q8_0, Q3_K, Q5_K, Q6_K, F32
 template <int TY>
 constexpr int dec_rows_per_pass() {
-    return (TY == T_Q8_0 || TY == T_Q6_K || TY == T_F32 || TY == T_Q5_K || TY == T_Q3_K) ? RIE_DEC_ROWS_LARGE : RIE_DEC_ROWS_SMALL;
+    return (TY == T_Q8_0 || TY == T_Q6_K || TY == T_F32 || TY == T_Q5_K || TY == T_Q3_K) ? 2 : 4;
 }
 
 constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
@@ -503,27 +499,6 @@ static int dec_units(int ty, int K) {
     return K / 64;
 }
 
-// Rows-per-workgroup multiplier override (0 = automatic), for launch-shape sweeps.
-static int dec_tile_override() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("RIE_HIP_GEMV_TILE");
-        v = e ? atoi(e) : 0;
-    }
-    return v;
-}
-
-// Rows per pass override for Q4_0 (tuning): 0 default, 1 eight rows for the
-// gate/up kernel with the Q8_0 hidden, 2 eight rows for every Q4_0 launch.
-static int dec_r8_mode() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("RIE_HIP_DEC_R8");
-        v = e ? atoi(e) : 0;
-    }
-    return v;
-}
-
 template <int TY, int R>
 static bool launch_dec_r(DecP p, hipStream_t st) {
     const int U = dec_units(TY, p.K);
@@ -543,8 +518,7 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         m = 1;
         if (nt > 1024) return false;
     } else {
-        const int ov = dec_tile_override();
-        m = ov > 0 ? ov : std::max(1, std::min(4, p.total_rows / (pass * 1024)));
+        m = std::max(1, std::min(4, p.total_rows / (pass * 1024)));
     }
     p.tr = pass * m;
     if (p.xsel && p.slot_rows % p.tr) {  // a workgroup must not straddle two experts
@@ -583,10 +557,6 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
 
 template <int TY>
 static bool launch_dec_t(const DecP &p, hipStream_t st) {
-    if constexpr (TY == T_Q4_0) {
-        const int m = dec_r8_mode();
-        if (m == 2 || (m == 1 && p.glu && p.hq.qs)) return launch_dec_r<TY, 8>(p, st);
-    }
     return launch_dec_r<TY, dec_rows_per_pass<TY>()>(p, st);
 }
 
