@@ -1033,15 +1033,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
         }
     }
     __shared__ int s_last;
-    // Every thread's partial stores have completed (device-visible) before the
-    // barrier, so the arrival count never runs ahead of the data it announces.
+    // Publication of the partials: every thread's stores complete before the
+    // barrier, and the arrival count is an agent-scope release, so in the HIP
+    // memory model the stores of all ranges happen-before the last arrival's
+    // acquire fence and the merge's loads after it (barrier, then release
+    // read-modify-write, then acquire fence on the value it returned).
     wait_vmem();
     __syncthreads();
     if (tid == 0) {
         int *cnt = a.counters + blockIdx.y * ATT_CNT_STRIDE;  // one 128-byte line per head slice: no contention between slices
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == ns - 1;
-        if (old == ns - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == ns - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     __syncthreads();
     if (!s_last) return;
