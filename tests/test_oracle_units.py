@@ -105,6 +105,174 @@ def test_q4_0_known_block(oracle):
     assert list(y[16:]) == [float(15 - i - 8) for i in range(16)]
 
 
+# Hand-built blocks for every other block layout.  Each block's fields are
+# literal bytes chosen so that every scale, min, code and high bit differs from
+# its neighbours; the expected values are read off the layouts of
+# quant/reference.rs:8-215 by hand (scale/min unpacking: get_scale_min_k4 8-14,
+# unpack_q3k_scales 30-51) and written either as literals or as the closed form
+# "element i = scale(i)·code(i) − min(i)" of this particular block, so an index,
+# nibble or shift slip in the oracle (or in the ggml_np transcription it is
+# compared with) fails here.  d and min are powers of two: every expected value
+# is exact in f32.
+def _f16b(v):
+    return list(np.array([v], np.float16).view(np.uint8))
+
+
+def test_q4_1_known_block(oracle):
+    # d = 0.5, m = -3.0, qs[j]: low nibble j, high nibble 15 - j
+    blk = np.array(_f16b(0.5) + _f16b(-3.0) + [j | (15 - j) << 4 for j in range(16)], np.uint8)
+    y = oracle.dequantize_row(3, blk, 32)
+    assert np.array_equal(G.dequantize(3, blk, 32), y)  # the numpy transcription too
+    assert list(y[:16]) == [j * 0.5 - 3 for j in range(16)]
+    assert list(y[16:]) == [(15 - j) * 0.5 - 3 for j in range(16)]
+    assert y[0] == -3.0 and y[15] == 4.5 and y[16] == 4.5 and y[31] == -3.0
+
+
+def test_q5_0_known_block(oracle):
+    # d = 1, qh = 0xFF005555 (bit j set for even j < 16, bits 24..31 set), qs[j] = j | (15-j) << 4
+    blk = np.array(_f16b(1.0) + [0x55, 0x55, 0x00, 0xFF] + [j | (15 - j) << 4 for j in range(16)], np.uint8)
+    y = oracle.dequantize_row(6, blk, 32)
+    assert np.array_equal(G.dequantize(6, blk, 32), y)  # the numpy transcription too
+    assert list(y[:16]) == [float(j if j % 2 == 0 else j - 16) for j in range(16)]
+    assert list(y[16:]) == [float(-1 - j if j < 8 else 15 - j) for j in range(16)]
+    assert list(y[:4]) == [0.0, -15.0, 2.0, -13.0] and list(y[22:26]) == [-7.0, -8.0, 7.0, 6.0]
+
+
+def test_q5_1_known_block(oracle):
+    # d = 0.25, m = 1, qh = 0x0F0F0F0F (bits 0-3, 8-11, 16-19, 24-27), qs[j] = (15-j) | j << 4
+    blk = np.array(_f16b(0.25) + _f16b(1.0) + [0x0F] * 4 + [(15 - j) | j << 4 for j in range(16)], np.uint8)
+    y = oracle.dequantize_row(7, blk, 32)
+    assert np.array_equal(G.dequantize(7, blk, 32), y)  # the numpy transcription too
+    hi = [16 if j % 8 < 4 else 0 for j in range(16)]
+    assert list(y[:16]) == [((15 - j) + hi[j]) * 0.25 + 1 for j in range(16)]
+    assert list(y[16:]) == [(j + hi[j]) * 0.25 + 1 for j in range(16)]
+    assert y[0] == 8.75 and y[4] == 3.75 and y[16] == 5.0 and y[31] == 4.75
+
+
+def test_q2_k_known_block(oracle):
+    # scales[i] = i | (15 - i) << 4 (scale i, min 15 - i); code bytes 0xE4 (2-bit codes
+    # 0,1,2,3 at shifts 0,2,4,6) at even and 0x1B (3,2,1,0) at odd positions; d = 1, min = 0.5
+    blk = np.array([i | (15 - i) << 4 for i in range(16)] + [0xE4, 0x1B] * 32 + _f16b(1.0) + _f16b(0.5), np.uint8)
+    assert blk.size == 84
+    y = oracle.dequantize_row(10, blk, 256)
+    assert np.array_equal(G.dequantize(10, blk, 256), y)  # the numpy transcription too
+    for n in range(2):
+        for it in range(4):
+            for half in range(2):
+                for l in range(16):
+                    i = n * 8 + it * 2 + half
+                    code = it if l % 2 == 0 else 3 - it
+                    assert y[n * 128 + it * 32 + half * 16 + l] == i * code - 0.5 * (15 - i), (n, it, half, l)
+    assert y[0] == -7.5 and y[1] == 0 * 3 - 7.5 and y[32 + 1] == 2 * 2 - 6.5 and y[254] == 15 * 3 - 0.0 and y[255] == 0.0
+
+
+def test_q3_k_known_block(oracle):
+    # 16 six-bit scales (before the -32 offset) 33 30 40 20 50 10 60 5 34 29 47 16 63 0 36 28,
+    # packed as unpack_q3k_scales reads them: low nibbles of scales 0-7 / high nibbles of 8-15
+    # in bytes 0-7, the top two bits of scales i, 4+i, 8+i, 12+i in byte 8+i
+    sc_bytes = [0x21, 0xDE, 0xF8, 0x04, 0xF2, 0x0A, 0x4C, 0xC5, 0xEE, 0x11, 0xAE, 0x51]
+    scales = [1, -2, 8, -12, 18, -22, 28, -27, 2, -3, 15, -16, 31, -32, 4, -4]
+    hm = [0xA5 if i % 2 == 0 else 0x5A for i in range(32)]
+    # 2-bit codes: 0xE4 (code = shift step) in the first 16 bytes of each 32-byte half, 0x1B
+    # (3 - step) in the second; swapped for the second half
+    q = [0xE4] * 16 + [0x1B] * 16 + [0x1B] * 16 + [0xE4] * 16
+    blk = np.array(hm + q + sc_bytes + _f16b(1.0), np.uint8)
+    assert blk.size == 110
+    y = oracle.dequantize_row(11, blk, 256)
+    assert np.array_equal(G.dequantize(11, blk, 256), y)  # the numpy transcription too
+    for n in range(2):
+        for it in range(4):
+            for half in range(2):
+                for l in range(16):
+                    code = it if (half == 0) != (n == 1) else 3 - it
+                    bit = (hm[l + 16 * half] >> (n * 4 + it)) & 1
+                    want = scales[n * 8 + it * 2 + half] * (code - (0 if bit else 4))
+                    assert y[n * 128 + it * 32 + half * 16 + l] == want, (n, it, half, l)
+    # element 0: scale 1, code 0, hm bit 0 of 0xA5 set -> 0; element 1: hm 0x5A bit 0 clear -> 1·(0-4);
+    # element 255: scale -4, code 3, bit 7 of 0x5A clear -> -4·(3-4)
+    assert y[0] == 0.0 and y[1] == -4.0 and y[16] == -2 * 3 and y[255] == 4.0
+
+
+# sc = 1 2 3 4 37 54 7 63, m = 9 10 11 12 45 22 19 50, packed as get_scale_min_k4 reads them
+K4_SCALES = [0x81, 0xC2, 0x03, 0xC4, 0x89, 0x4A, 0x4B, 0xCC, 0xD5, 0x66, 0x37, 0x2F]
+K4_SC, K4_M = [1, 2, 3, 4, 37, 54, 7, 63], [9, 10, 11, 12, 45, 22, 19, 50]
+
+
+def test_q4_k_known_block(oracle):
+    # d = 1, dmin = 0.5; code byte 32j+l: low nibble l % 16, high nibble (l + 5j) % 16
+    qs = [(l % 16) | ((l + 5 * j) % 16) << 4 for j in range(4) for l in range(32)]
+    blk = np.array(_f16b(1.0) + _f16b(0.5) + K4_SCALES + qs, np.uint8)
+    assert blk.size == 144
+    y = oracle.dequantize_row(12, blk, 256)
+    assert np.array_equal(G.dequantize(12, blk, 256), y)  # the numpy transcription too
+    for j in range(4):
+        for l in range(32):
+            assert y[64 * j + l] == K4_SC[2 * j] * (l % 16) - 0.5 * K4_M[2 * j], (j, l)
+            assert y[64 * j + 32 + l] == K4_SC[2 * j + 1] * ((l + 5 * j) % 16) - 0.5 * K4_M[2 * j + 1], (j, l)
+    assert y[0] == -4.5 and y[128 + 32 + 1] == 54 * 11 - 11.0 and y[255] == 63 * 14 - 25.0
+
+
+def test_q5_k_known_block(oracle):
+    # as the Q4_K block, plus high bits qh[l] = 0x93 (bits 0,1,4,7) for even l, 0x6C (2,3,5,6) for odd l
+    qh = [0x93 if l % 2 == 0 else 0x6C for l in range(32)]
+    ql = [(l % 16) | ((l + 5 * j) % 16) << 4 for j in range(4) for l in range(32)]
+    blk = np.array(_f16b(1.0) + _f16b(0.5) + K4_SCALES + qh + ql, np.uint8)
+    assert blk.size == 176
+    y = oracle.dequantize_row(13, blk, 256)
+    assert np.array_equal(G.dequantize(13, blk, 256), y)  # the numpy transcription too
+    for j in range(4):
+        for l in range(32):
+            h1 = 16 * ((qh[l] >> (2 * j)) & 1)
+            h2 = 16 * ((qh[l] >> (2 * j + 1)) & 1)
+            assert y[64 * j + l] == K4_SC[2 * j] * ((l % 16) + h1) - 0.5 * K4_M[2 * j], (j, l)
+            assert y[64 * j + 32 + l] == K4_SC[2 * j + 1] * (((l + 5 * j) % 16) + h2) - 0.5 * K4_M[2 * j + 1], (j, l)
+    # element 0: qh[0] bit 0 set -> 1·(0+16) - 4.5; element 1: qh[1] = 0x6C bit 0 clear -> 1·1 - 4.5
+    assert y[0] == 11.5 and y[1] == -3.5 and y[255] == 63 * (14 + 0) - 25.0
+
+
+def test_q6_k_known_block(oracle):
+    # ql[k]: low nibble k % 16, high nibble k // 16; qh[k] = 0xE4 for k < 32 (2-bit fields
+    # 0,1,2,3), 0x1B for k >= 32 (3,2,1,0); signed scales 1 -2 3 -4 ... 15 -16; d = 1
+    ql = [(k % 16) | (k // 16) << 4 for k in range(128)]
+    qh = [0xE4] * 32 + [0x1B] * 32
+    sc = [(i + 1) * (1 if i % 2 == 0 else -1) for i in range(16)]
+    blk = np.array(ql + qh + [v & 0xFF for v in sc] + _f16b(1.0), np.uint8)
+    assert blk.size == 210
+    y = oracle.dequantize_row(14, blk, 256)
+    assert np.array_equal(G.dequantize(14, blk, 256), y)  # the numpy transcription too
+    for n in range(2):
+        p = (0, 1, 2, 3) if n == 0 else (3, 2, 1, 0)
+        for l in range(32):
+            i = l // 16
+            q1 = (l % 16) | p[0] << 4
+            q2 = (l % 16) | p[1] << 4
+            q3 = (4 * n + l // 16) | p[2] << 4
+            q4 = (4 * n + 2 + l // 16) | p[3] << 4
+            assert y[128 * n + l] == sc[8 * n + i] * (q1 - 32), (n, l)
+            assert y[128 * n + l + 32] == sc[8 * n + i + 2] * (q2 - 32), (n, l)
+            assert y[128 * n + l + 64] == sc[8 * n + i + 4] * (q3 - 32), (n, l)
+            assert y[128 * n + l + 96] == sc[8 * n + i + 6] * (q4 - 32), (n, l)
+    assert y[0] == -32.0 and y[255] == -16 * (7 - 32) and y[64] == 5 * (0 | 2 << 4) - 5 * 32
+
+
+def test_turbo4_known_row(oracle):
+    """quantize_rotated_4 (turbo.rs:140-164) on a hand-built rotated row of 128
+    values: chunk c holds P[(g + 3c) % 8] in its first 16 values and -P[...] in
+    its last 16, P = (2, -2, 1, -1, 0.5, -0.5, 0, 0).  rms = sqrt(1.3125); y/rms
+    lands on levels 74, -74, 43, -43, 18, -18 and, for 0 (not above the zero
+    midpoint), -6: codes 13, 2, 11, 4, 9, 6, 7.  The least-squares scale is
+    (Σ y·c)/(Σ c²) = 46·400/15370 = 1.19714 -> f16 0x3CCA.  Codes go in Q4_0
+    nibble order: byte 16c + j holds value 32c + j (low) and 32c + 16 + j (high)."""
+    P = [2.0, -2.0, 1.0, -1.0, 0.5, -0.5, 0.0, 0.0]
+    y = np.array([P[(g + 3 * (g // 32)) % 8] * (1 if g % 32 < 16 else -1) for g in range(128)], np.float32)
+    out = np.zeros(66, np.uint8)
+    oracle.lib().or_turbo_quantize_rotated(oracle.ptr(y), 128, oracle.ptr(out))
+    T = [0x2D, 0xD2, 0x4B, 0xB4, 0x69, 0x96, 0x77, 0x77]
+    assert list(out[:2]) == [0xCA, 0x3C]
+    assert list(out[2:]) == [T[(j + 3 * c) % 8] for c in range(4) for j in range(16)]
+    assert oracle.turbo_row_bytes(128) == 66 and oracle.turbo_row_bytes(96) == 54  # turbo.rs:571-572
+
+
 # ---- activation quantizers ---------------------------------------------------------------
 def test_q8_0_known_answers(oracle):
     x = np.zeros(64, np.float32)
