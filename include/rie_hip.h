@@ -163,6 +163,15 @@ int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
                        const int32_t *isum, const int16_t *bsums, int32_t n_tok, float *out);
 /* greedy argmax (sampler.rs:199-209) of n floats */
 int32_t rie_hip_k_argmax(const float *x, int32_t n, uint32_t *out_idx);
+/* The same argmax without allocating device memory.  No counterpart in the
+ * reference: for callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The partial
+ * maxima live in a fixed 8 KiB array of the library's static device memory (one
+ * copy per GPU, held until the process ends), so n must be in 1..1048576
+ * (1024 partials of up to 1024 values); larger or empty inputs return
+ * RIE_HIP_ERR_RUNTIME with the reason in err.  Calls that overlap on one GPU
+ * (from several host threads) share that array and race. */
+int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, char *err, size_t err_len);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,7 @@ def lib():
         "rie_hip_k_gemv": (I, [I, P, I, I, P, P, P, P, P, P, I, P]),
         "rie_hip_k_gemm": (I, [I, P, I, I, P, P, P, P, P, I, P]),
         "rie_hip_k_argmax": (I, [P, I, P]),
+        "rie_hip_k_argmax_noalloc": (I, [P, I, P, CP, S]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -291,4 +291,12 @@ int32_t rie_hip_k_argmax(const float *x, int32_t n, uint32_t *out_idx) {
     });
 }
 
+int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, char *err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        rie::launch_argmax_noalloc(x, n, out_idx, 0);
+        RIE_HIP_CHECK(hipGetLastError());
+        RIE_HIP_CHECK(hipDeviceSynchronize());
+    });
+}
+
 }  // extern "C"

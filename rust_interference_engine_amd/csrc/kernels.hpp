@@ -99,6 +99,11 @@ int attention_splits(int n_tok, int n_kv, int max_len);
 
 // ---- misc.hip ----
 void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st);
+// The same argmax with its partials in the library's static device array (no
+// allocation); n in 1..ARGMAX_SCRATCH_PARTS·ARGMAX_SCRATCH_PER_PART, else throws.
+// Calls that overlap on one GPU share the array and race.
+constexpr int ARGMAX_SCRATCH_PARTS = 1024, ARGMAX_SCRATCH_PER_PART = 1024;
+void launch_argmax_noalloc(const float *x, int n, uint32_t *out_idx, hipStream_t st);
 void launch_add_inplace(float *x, const float *y, size_t n, float scale, hipStream_t st);
 void launch_scale(float *x, size_t n, float div, hipStream_t st);
 void launch_set_int(int *p, int v, hipStream_t st);

@@ -3,6 +3,9 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <mutex>
+#include <string>
+
 namespace rie {
 
 // sampler.rs:199-209: the first index holding the strict maximum.  NaN never wins.
@@ -53,6 +56,47 @@ __global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float
 void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st) {
     hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
     hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx);
+}
+
+// ---- argmax without device allocation ----
+// The partial maxima live in one fixed array of the library's static device
+// memory: ARGMAX_SCRATCH_PARTS (index, value) pairs, [idx × PARTS][val × PARTS].
+// Each GPU holds its own copy of the array until the process ends; the host
+// never uses the symbol itself as an address, only the per-device address that
+// hipGetSymbolAddress returns for it.  Nothing in it must start at zero: stage 1
+// writes every partial that stage 2 reads.
+static __device__ __align__(256) unsigned char scratch[ARGMAX_SCRATCH_PARTS * 8];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_dev[MAX_DEVICES];  // device address of `scratch` on each GPU, looked up once
+
+void *scratch_for_current_device() {
+    int dev = -1;
+    RIE_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) throw Error{E_RUNTIME, "device ordinal " + std::to_string(dev) + " out of range"};
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            throw Error{E_RUNTIME, std::string("hipGetSymbolAddress of the argmax scratch array failed: ") + hipGetErrorString(e)};
+        scratch_dev[dev] = p;
+    }
+    return scratch_dev[dev];
+}
+}  // namespace
+
+void launch_argmax_noalloc(const float *x, int n, uint32_t *out_idx, hipStream_t st) {
+    if (n < 1 || n > ARGMAX_SCRATCH_PARTS * ARGMAX_SCRATCH_PER_PART)
+        throw Error{E_RUNTIME, "argmax without allocation: " + std::to_string(n) + " values is outside 1.." +
+                                   std::to_string(ARGMAX_SCRATCH_PARTS * ARGMAX_SCRATCH_PER_PART) + " (the scratch holds " +
+                                   std::to_string(ARGMAX_SCRATCH_PARTS) + " partials of up to " +
+                                   std::to_string(ARGMAX_SCRATCH_PER_PART) + " values)"};
+    unsigned char *base = (unsigned char *)scratch_for_current_device();
+    const int n_part = (n + ARGMAX_SCRATCH_PER_PART - 1) / ARGMAX_SCRATCH_PER_PART;
+    launch_argmax(x, n, (int *)base, (float *)(base + ARGMAX_SCRATCH_PARTS * 4), n_part, out_idx, st);
 }
 
 __global__ void add_kernel(float *x, const float *y, size_t n, float scale) {
