@@ -114,6 +114,10 @@ typedef struct rie_hip_synth_spec {
     int32_t mode;
     float rope_base;
     int32_t output_type; /* mode 1: type of output.weight (-1 = embd_type) */
+    /* mode 1 per-tensor mix: 0 = every matrix wtype; 1 = Q4_K_M: attn_v Q6_K, ffn_down
+     * Q6_K in the layers llama.cpp's Q4_K_M gives more bits (i < n/8, i >= 7n/8,
+     * (i - n/8) % 3 == 2), wtype elsewhere */
+    int32_t mix;
 } rie_hip_synth_spec;
 
 /* SyntheticSpec::tiny (testing.rs:127-154) / preset (testing.rs:157-212); 0 or -1. */
@@ -123,6 +127,12 @@ int32_t rie_hip_synth_preset(const char *name, int32_t wtype, rie_hip_synth_spec
  * owned by the library (release with rie_hip_free); returns its size, 0 on error. */
 size_t rie_hip_synth_build(const rie_hip_synth_spec *spec, uint8_t **out, int32_t n_threads);
 void rie_hip_free(void *p);
+/* The generator's weight quantizers: n values of x to ggml blocks of type ty
+ * (Q4_0 and Q8_0 are quantize::q4_0 / quantize::q8_0, quant/mod.rs:262-298;
+ * Q4_K and Q6_K, which the reference has no quantizer for, are min/max
+ * quantizers of this library).  0, or RIE_HIP_ERR_UNSUPPORTED for other types
+ * or n not a multiple of the block size. */
+int32_t rie_hip_quantize(int32_t ty, const float *x, size_t n, uint8_t *out);
 
 /* ---- parity hooks (no counterpart in the reference; for tests and debugging) ---- */
 /* Keep per-layer copies of intermediate f32 tensors during forward (slow path):

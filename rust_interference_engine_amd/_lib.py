@@ -21,7 +21,7 @@ class SynthSpec(C.Structure):
         ("qk_norm", C.c_int32), ("post_norms", C.c_int32), ("fused", C.c_int32),
         ("swa_window", C.c_uint32), ("n_expert", C.c_uint32), ("n_expert_used", C.c_uint32),
         ("n_ff_exp", C.c_uint32), ("n_ff_shexp", C.c_uint32), ("chat_template", C.c_int32), ("seed", C.c_uint64),
-        ("mode", C.c_int32), ("rope_base", C.c_float), ("output_type", C.c_int32)]
+        ("mode", C.c_int32), ("rope_base", C.c_float), ("output_type", C.c_int32), ("mix", C.c_int32)]
 
 
 class Config(C.Structure):
@@ -63,6 +63,7 @@ def lib():
         "rie_hip_synth_preset": (I, [CP, I, C.POINTER(SynthSpec)]),
         "rie_hip_synth_build": (S, [C.POINTER(SynthSpec), U8P, I]),
         "rie_hip_free": (None, [P]),
+        "rie_hip_quantize": (I, [I, P, S, P]),
         "rie_hip_set_capture": (I, [P, I]),
         "rie_hip_capture": (I, [P, S, I, P, S]),
         "rie_hip_kv_layer": (I, [P, S, I, P, S, P, S]),

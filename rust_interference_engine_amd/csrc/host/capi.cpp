@@ -180,6 +180,10 @@ size_t rie_hip_synth_build(const rie_hip_synth_spec *spec, uint8_t **out, int32_
 
 void rie_hip_free(void *p) { free(p); }
 
+int32_t rie_hip_quantize(int32_t ty, const float *x, size_t n, uint8_t *out) {
+    return rie::synth_quantize(ty, x, n, out) ? RIE_HIP_OK : RIE_HIP_ERR_UNSUPPORTED;
+}
+
 int32_t rie_hip_set_capture(rie_hip_backend *b, int32_t on) {
     return guarded(nullptr, 0, [&] { b->b->set_capture(on != 0); });
 }

@@ -6,13 +6,15 @@
 // 1 + 0.1·U(-1,1); the metadata, vocabulary and tensor order are the same, and
 // the image layout is GgufWriter::to_bytes (gguf.rs:407-436, 32-byte alignment).
 //
-// mode 1 is the BASELINE workload definition: weights drawn N(0, 0.02) (normal
-// quantiles looked up with 16-bit uniforms, see Normal below) and
-// quantized with the reference's own quantize::q4_0 / quantize::q8_0
-// (quant/mod.rs:262-298), unit norms, a chosen RoPE base, a chosen output-head
-// type.  Each tensor is cut into 64-row chunks with independent Rng streams
-// seeded by splitmix64(seed, tensor index, chunk index), so the image is
-// generated in parallel and is the same for any thread count.
+// mode 1 is the benchmark workload definition: weights drawn N(0, 0.02) (normal
+// quantiles looked up with 16-bit uniforms, see Normal below) and quantized
+// with the reference's own quantize::q4_0 / quantize::q8_0 (quant/mod.rs:
+// 262-298) or, for Q4_K and Q6_K (which the reference cannot produce,
+// quant/mod.rs:259-261), with the min/max quantizers below; unit norms, a
+// chosen RoPE base, a chosen output-head type, and optionally the Q4_K_M
+// per-tensor mix.  Each tensor is cut into 64-row chunks with independent Rng
+// streams seeded by splitmix64(seed, tensor index, chunk index), so the image
+// is generated in parallel and is the same for any thread count.
 #include "synth.hpp"
 
 #include "../common.hpp"
@@ -167,6 +169,126 @@ void quantize_q8_0(const float *x, size_t n, uint8_t *out) {
         }
     }
 }
+
+int nearest_int(float v) { return (int)std::nearbyint(v); }  // round half to even
+
+float h2f_host(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) bits = sign;
+        else {  // subnormal: renormalize
+            int e = -1;
+            uint32_t m = man;
+            do { m <<= 1; e++; } while (!(m & 0x400u));
+            bits = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (exp == 0x1f) bits = sign | 0x7f800000u | (man << 13);
+    else bits = sign | ((exp + 112) << 23) | (man << 13);
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Q4_K (256 values: 8 sub-blocks of 32, 6-bit scale and min each, f16 d and
+// dmin; layout of dequantize_block, quant/reference.rs:8-27, 160-176).  Per
+// sub-block: min = −min(0, x), scale = (max − min(0, x)) / 15; d and dmin are the
+// largest scale and min over 63, the 6-bit sub-block values the nearest
+// multiples of the stored f16 d and dmin, and each code the nearest level
+// d·sc·q − dmin·m, q in 0..15.
+void quantize_q4_k(const float *x, size_t n, uint8_t *out) {
+    for (size_t b = 0; b < n / 256; b++) {
+        const float *xb = x + b * 256;
+        uint8_t *o = out + b * 144;
+        float scale[8], mn[8];
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            float lo = 0.0f, hi = -INFINITY;
+            for (int l = 0; l < 32; l++) {
+                lo = std::fmin(lo, xb[32 * j + l]);
+                hi = std::fmax(hi, xb[32 * j + l]);
+            }
+            scale[j] = (hi - lo) / 15.0f;
+            mn[j] = -lo;
+            max_scale = std::fmax(max_scale, scale[j]);
+            max_min = std::fmax(max_min, mn[j]);
+        }
+        const uint16_t dh = f2h(max_scale / 63.0f), mh = f2h(max_min / 63.0f);
+        const float d = h2f_host(dh), dmin = h2f_host(mh);
+        uint8_t sc[8], m[8];
+        for (int j = 0; j < 8; j++) {
+            sc[j] = (uint8_t)std::min(63, std::max(0, d > 0.0f ? nearest_int(scale[j] / d) : 0));
+            m[j] = (uint8_t)std::min(63, std::max(0, dmin > 0.0f ? nearest_int(mn[j] / dmin) : 0));
+        }
+        put16(o, dh);
+        put16(o + 2, mh);
+        // the 12-byte field as get_scale_min_k4 reads it: bytes 0-3 scales 0-3 with the top
+        // two bits of scales 4-7, bytes 4-7 mins 0-3 with the top bits of mins 4-7, bytes
+        // 8-11 the low nibbles of scales 4-7 (low) and mins 4-7 (high)
+        for (int j = 0; j < 4; j++) {
+            o[4 + j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+            o[8 + j] = (uint8_t)(m[j] | ((m[j + 4] >> 4) << 6));
+            o[12 + j] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+        }
+        uint8_t q[256];
+        for (int j = 0; j < 8; j++) {
+            const float ds = d * (float)sc[j], dm = dmin * (float)m[j];
+            for (int l = 0; l < 32; l++) {
+                const int v = ds > 0.0f ? nearest_int((xb[32 * j + l] + dm) / ds) : 0;
+                q[32 * j + l] = (uint8_t)std::min(15, std::max(0, v));
+            }
+        }
+        // byte 32j + l: value 64j + l (low nibble), value 64j + 32 + l (high nibble)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) o[16 + 32 * j + l] = (uint8_t)(q[64 * j + l] | (q[64 * j + 32 + l] << 4));
+    }
+}
+
+// Q6_K (256 values: 16 sub-blocks of 16 with signed 8-bit scales, f16 d; layout
+// of quant/reference.rs:190-212).  Per sub-block the value of largest
+// magnitude maps to code −32 (scale = that value / −32); d is the largest |scale|
+// over 127, the sub-block scales the nearest multiples of the stored f16 d, and
+// each code the nearest d·sc·q, q in −32..31 (stored +32).
+void quantize_q6_k(const float *x, size_t n, uint8_t *out) {
+    for (size_t b = 0; b < n / 256; b++) {
+        const float *xb = x + b * 256;
+        uint8_t *o = out + b * 210;
+        float scale[16];
+        float amax_scale = 0.0f;
+        for (int k = 0; k < 16; k++) {
+            float mx = 0.0f;
+            for (int l = 0; l < 16; l++)
+                if (std::fabs(xb[16 * k + l]) > std::fabs(mx)) mx = xb[16 * k + l];
+            scale[k] = mx / -32.0f;
+            amax_scale = std::fmax(amax_scale, std::fabs(scale[k]));
+        }
+        const uint16_t dh = f2h(amax_scale / 127.0f);
+        const float d = h2f_host(dh);
+        int8_t sc[16];
+        for (int k = 0; k < 16; k++) sc[k] = (int8_t)std::min(127, std::max(-127, d > 0.0f ? nearest_int(scale[k] / d) : 0));
+        uint8_t q[256];
+        for (int k = 0; k < 16; k++) {
+            const float ds = d * (float)sc[k];
+            for (int l = 0; l < 16; l++) {
+                const int v = ds != 0.0f ? nearest_int(xb[16 * k + l] / ds) : 0;
+                q[16 * k + l] = (uint8_t)(std::min(31, std::max(-32, v)) + 32);
+            }
+        }
+        uint8_t *ql = o, *qh = o + 128;
+        for (int h = 0; h < 2; h++)
+            for (int l = 0; l < 32; l++) {
+                const uint8_t q1 = q[128 * h + l], q2 = q[128 * h + l + 32], q3 = q[128 * h + l + 64], q4 = q[128 * h + l + 96];
+                ql[64 * h + l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+                ql[64 * h + l + 32] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+                qh[32 * h + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+        for (int k = 0; k < 16; k++) o[192 + k] = (uint8_t)sc[k];
+        put16(o + 208, dh);
+    }
+}
+
+// llama.cpp's choice of the layers that get the larger type in a Q4_K_M file
+bool more_bits_layer(uint32_t i, uint32_t n) { return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2; }
 
 uint64_t splitmix(uint64_t z) {
     z += 0x9E3779B97F4A7C15ULL;
@@ -371,6 +493,8 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
         w.kv_f32("granite.attention.scale", 0.0078125f * 8.0f);
     }
     if (a == "gemma3") w.kv_f32("gemma3.rope.freq_base", 1000000.0f);
+    // mode 1 records the weight mix as llama.cpp's general.file_type (2 Q4_0, 7 Q8_0, 15 Q4_K_M, 14 Q4_K_S)
+    if (m1) w.kv_u32("general.file_type", sp.mix == 1 ? 15u : sp.wtype == T_Q4_K ? 14u : sp.wtype == T_Q8_0 ? 7u : 2u);
     // vocabulary (testing.rs:264-300)
     std::vector<std::string> toks = {"<unk>", "<s>", "</s>"};
     std::vector<int32_t> types = {2, 3, 3};
@@ -442,7 +566,7 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
         else {
             add(p + "attn_q.weight", {e, qd}, wt, qd, e, 0, 0);
             add(p + "attn_k.weight", {e, kvd}, wt, kvd, e, 0, 0);
-            add(p + "attn_v.weight", {e, kvd}, wt, kvd, e, 0, 0);
+            add(p + "attn_v.weight", {e, kvd}, (m1 && sp.mix == 1) ? T_Q6_K : wt, kvd, e, 0, 0);
         }
         if (sp.qkv_bias) {
             add(p + "attn_q.bias", {qd}, T_F32, 1, qd, 2, 0.1f);
@@ -454,6 +578,7 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
             add(p + "attn_k_norm.weight", {hd}, T_F32, 1, hd, 1, 0);
         }
         add(p + "attn_output.weight", {qd, e}, wt, e, qd, 0, 0);
+        const int down_ty = (m1 && sp.mix == 1 && more_bits_layer(il, sp.n_layer)) ? T_Q6_K : wt;
         if (sp.post_norms) {
             add(p + "post_attention_norm.weight", {e}, T_F32, 1, e, 1, 0);
             add(p + "post_ffw_norm.weight", {e}, T_F32, 1, e, 1, 0);
@@ -478,12 +603,12 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
         } else {
             add(p + "ffn_gate.weight", {e, ff}, wt, ff, e, 0, 0);
             add(p + "ffn_up.weight", {e, ff}, wt, ff, e, 0, 0);
-            add(p + "ffn_down.weight", {ff, e}, wt, e, ff, 0, 0);
+            add(p + "ffn_down.weight", {ff, e}, down_ty, e, ff, 0, 0);
         }
     }
     if (m1)
         for (auto &p : plans)
-            if ((p.kind == 0) && !(p.ty == T_Q4_0 || p.ty == T_Q8_0 || p.ty == T_F32 || p.ty == T_F16))
+            if ((p.kind == 0) && !(p.ty == T_Q4_0 || p.ty == T_Q8_0 || p.ty == T_Q4_K || p.ty == T_Q6_K || p.ty == T_F32 || p.ty == T_F16))
                 throw Error{E_UNSUPPORTED, std::string("unsupported: N(0,0.02) synthesis of type ") + type_name(p.ty)};
     // ---- layout (gguf.rs:407-436) ----
     std::vector<uint8_t> hdr;
@@ -572,6 +697,8 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
             switch (p.ty) {
             case T_Q4_0: quantize_q4_0(vals.data(), n, o); break;
             case T_Q8_0: quantize_q8_0(vals.data(), n, o); break;
+            case T_Q4_K: quantize_q4_k(vals.data(), n, o); break;
+            case T_Q6_K: quantize_q6_k(vals.data(), n, o); break;
             case T_F16:
                 for (size_t i = 0; i < n; i++) put16(o + 2 * i, f2h(vals[i]));
                 break;
@@ -586,6 +713,16 @@ uint8_t *synth_build(const rie_hip_synth_spec &sp, int n_threads, size_t *out_le
     worker();
     for (auto &t : th) t.join();
     return img;
+}
+
+bool synth_quantize(int ty, const float *x, size_t n, uint8_t *out) {
+    switch (ty) {
+    case T_Q4_0: if (n % 32) return false; quantize_q4_0(x, n, out); return true;
+    case T_Q8_0: if (n % 32) return false; quantize_q8_0(x, n, out); return true;
+    case T_Q4_K: if (n % 256) return false; quantize_q4_k(x, n, out); return true;
+    case T_Q6_K: if (n % 256) return false; quantize_q6_k(x, n, out); return true;
+    default: return false;
+    }
 }
 
 }  // namespace rie

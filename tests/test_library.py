@@ -94,3 +94,107 @@ def test_kv_type_parse():
 def test_argmax_first_max():
     assert R.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
     assert R.argmax(np.array([np.nan, 1, 1], np.float32)) == 1
+
+
+# ---- the workload generator's quantizers (mode 1) ------------------------------------
+def test_quantize_q4_0_q8_0_equal_reference_quantizers(oracle):
+    """quantize::q4_0 / q8_0 (quant/mod.rs:262-298): the generator's bytes equal the oracle's restatement."""
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(32 * 300) * rng.uniform(0.001, 3, 32 * 300)).astype(np.float32)
+    x[:32] = 0
+    for ty in (synth.Q4_0, synth.Q8_0):
+        assert np.array_equal(synth.quantize(ty, x), oracle.quantize_weights(ty, x)), ty
+
+
+def _q6_k_representable(rng, nb):
+    """blocks whose values are exactly d·sc·q: per superblock d = 2^-10 (f16 exact), one
+    sub-block scale of magnitude 127, and in every sub-block the largest magnitude at code -32"""
+    x = np.zeros((nb, 16, 16), np.float32)
+    for b in range(nb):
+        sc = rng.integers(-127, 128, 16)
+        sc[sc == 0] = 5
+        sc[rng.integers(16)] = 127 * (1 if rng.random() < 0.5 else -1)
+        for k in range(16):
+            q = rng.integers(-31, 32, 16)
+            q[rng.integers(16)] = -32
+            x[b, k] = np.float32(2.0 ** -10) * np.float32(sc[k]) * q.astype(np.float32)
+    return x.reshape(-1)
+
+
+def _q4_k_representable(rng, nb):
+    """values d·sc·q - dmin·m with d = 2^-6, dmin = 2^-7, codes 0 and 15 present in every
+    sub-block, scale 63 and min 63 present in every superblock: all exact in f32"""
+    x = np.zeros((nb, 8, 32), np.float32)
+    for b in range(nb):
+        sc = rng.integers(1, 64, 8)
+        m = rng.integers(1, 64, 8)
+        sc[rng.integers(8)] = 63
+        m[rng.integers(8)] = 63
+        for j in range(8):
+            q = rng.integers(0, 16, 32)
+            q[0], q[1] = 0, 15
+            rng.shuffle(q)
+            x[b, j] = np.float32(2.0 ** -6) * np.float32(sc[j]) * q.astype(np.float32) - np.float32(2.0 ** -7) * np.float32(m[j])
+    return x.reshape(-1)
+
+
+@pytest.mark.parametrize("ty", [synth.Q4_K, synth.Q6_K])
+def test_k_quantizers_reproduce_representable_blocks(oracle, ty):
+    """A block that the format holds exactly comes back exactly through the
+    oracle's dequantizer (itself pinned by hand-built blocks): this fixes the
+    generator's byte layout, scale packing and code placement."""
+    rng = np.random.default_rng(5 + ty)
+    x = (_q4_k_representable if ty == synth.Q4_K else _q6_k_representable)(rng, 12)
+    y = oracle.dequantize_row(ty, synth.quantize(ty, x), x.size)
+    assert np.array_equal(y, x)
+
+
+@pytest.mark.parametrize("ty,bound", [(synth.Q4_K, 0.12), (synth.Q6_K, 0.03)])
+def test_k_quantizers_error_on_gaussian_weights(oracle, ty, bound):
+    """N(0, 0.02) weights (the workload's): relative RMS error of the round trip
+    within the step size of the format (range/15 or amax/32 per sub-block)"""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(256 * 400) * 0.02).astype(np.float32)
+    y = oracle.dequantize_row(ty, synth.quantize(ty, x), x.size)
+    rel = np.sqrt(np.mean((y - x) ** 2)) / np.sqrt(np.mean(x ** 2))
+    assert rel < bound, rel
+    assert np.abs(y - x).max() < 0.25 * np.abs(x).max()
+
+
+def test_q4_k_m_mix_tensor_types(oracle):
+    """The Llama-3.2-3B Q4_K_M workload image: attn_v Q6_K in every layer, ffn_down Q6_K in
+    the 14 layers llama.cpp widens (i < 3, i >= 24, (i - 3) % 3 == 2 for 28 layers), Q4_K
+    elsewhere, tied Q6_K embeddings; the oracle loads the mixed-type image."""
+    from gguf_np import GGUF
+
+    s = synth.baseline_llama32_3b_q4_k_m()
+    s.n_vocab, s.n_embd, s.n_ff, s.n_head, s.n_head_kv = 512, 256, 512, 2, 1
+    g = GGUF(synth.build(s))
+    wide = {0, 1, 2, 5, 8, 11, 14, 17, 20, 23, 24, 25, 26, 27}
+    assert len(wide) == 14
+    for il in range(28):
+        assert g.tensors[f"blk.{il}.attn_v.weight"][0] == synth.Q6_K
+        assert g.tensors[f"blk.{il}.ffn_down.weight"][0] == (synth.Q6_K if il in wide else synth.Q4_K), il
+        for t in ("attn_q", "attn_k", "attn_output", "ffn_gate", "ffn_up"):
+            assert g.tensors[f"blk.{il}.{t}.weight"][0] == synth.Q4_K
+    assert g.tensors["token_embd.weight"][0] == synth.Q6_K and "output.weight" not in g.tensors
+    assert g.get("general.file_type") == 15 and abs(g.get("llama.rope.freq_base") - 5e5) < 1
+    m = oracle.Model(synth.build(s))
+    assert m.cfg["n_layer"] == 28
+
+
+def test_baseline_moe_image(oracle):
+    """The Qwen3-30B-A3B workload image: Q4_K experts, F32 N(0, 1) router, Q6_K embeddings and head."""
+    import ggml_np as G
+    from gguf_np import GGUF
+
+    s = synth.baseline_qwen3_30b_a3b_q4_k()
+    s.n_layer, s.n_vocab = 1, 512
+    g = GGUF(synth.build(s))
+    ty, dims, raw = g.tensors["blk.0.ffn_gate_inp.weight"]
+    r = G.dequantize(ty, raw, int(np.prod(dims)))
+    assert ty == 0 and list(dims) == [2048, 128] and abs(r.std() - 1.0) < 0.02
+    ty, dims, raw = g.tensors["blk.0.ffn_gate_exps.weight"]
+    w = G.dequantize(ty, raw, int(np.prod(dims)))
+    assert ty == synth.Q4_K and list(dims) == [2048, 768, 128] and abs(w.std() - 0.02) < 0.002
+    assert g.tensors["output.weight"][0] == synth.Q6_K and g.tensors["token_embd.weight"][0] == synth.Q6_K
