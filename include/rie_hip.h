@@ -137,7 +137,7 @@ int32_t rie_hip_quantize(int32_t ty, const float *x, size_t n, uint8_t *out);
 /* ---- parity hooks (no counterpart in the reference; for tests and debugging) ---- */
 /* Keep per-layer copies of intermediate f32 tensors during forward (slow path):
  * what = 0 x after attention, 1 x after FFN, 2 attention output, 3 q after
- * RoPE/scale, 4 k after norm/RoPE, 5 v, 6 FFN gated hidden. */
+ * RoPE/scale, 4 k after norm/RoPE, 5 v, 6 FFN gated hidden, 7 MoE router logits. */
 int32_t rie_hip_set_capture(rie_hip_backend *b, int32_t on);
 int32_t rie_hip_capture(rie_hip_backend *b, size_t layer, int32_t what, float *out, size_t len);
 /* Raw KV cache of one layer: which 0 = K, 1 = V; [kv_head][slot][row bytes];
@@ -161,7 +161,8 @@ int32_t rie_hip_time_ffn_glu(rie_hip_backend *b, int32_t reps, double *avg_us, s
 
 /* ---- kernel entry points on device pointers (stream 0, synchronous) ---- */
 /* RMSNorm (w may be NULL: quantize only) + Q8_0 (fmt 1) or Q8_K (fmt 2) quantization
- * of n rows of k values (quant/mod.rs:191-218, kernels/avx2.rs:153-184).  Outputs:
+ * of n rows of k values (ops.rs:7-14 with the sum of squares in the order of
+ * kernels/avx2.rs:186-203; quant/mod.rs:191-218, kernels/avx2.rs:153-184).  Outputs:
  * Q8_0: qs [n][k], d/s/isum [n][k/32]; Q8_K: qs [n][k], d [n][k/256], bsums [n][k/16]. */
 int32_t rie_hip_k_rmsnorm_quant(const float *x, const float *w, float eps, int32_t n, int32_t k, int32_t fmt, float *xn, int8_t *qs,
                                 float *d, float *s, int32_t *isum, int16_t *bsums);

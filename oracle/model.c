@@ -522,7 +522,7 @@ struct or_backend {
     acts_t acts;
     size_t hidden_rows;
     int capture;
-    float **cap[7];
+    float **cap[8];
 };
 
 static size_t kv_row_bytes(const or_backend *b) {
@@ -603,7 +603,7 @@ or_backend *or_backend_new(or_model *m, size_t n_ctx, size_t max_batch, int kv, 
 }
 
 static void free_capture(or_backend *b) {
-    for (int w = 0; w < 7; w++) {
+    for (int w = 0; w < 8; w++) {
         if (!b->cap[w]) continue;
         for (size_t il = 0; il < b->m->n_layer; il++)
             if (b->cap[w][il]) free((char *)b->cap[w][il] - 16);
@@ -806,11 +806,12 @@ static void dense_ffn(or_backend *b, const dense_t *d, const float *x, size_t n,
 }
 
 /* cpu.rs:473-524 */
-static void moe_ffn(or_backend *b, const moe_t *mo, const float *x, size_t n, float *out) {
+static void moe_ffn(or_backend *b, const moe_t *mo, const float *x, size_t n, float *out, size_t il) {
     size_t e = mo->router.cols, ne = mo->router.rows;
     const weight_t *wr = &mo->router;
     acts_prepare(b->pool, &b->acts, x, n, e, &wr, 1);
     matmul1(b->pool, &b->acts, &mo->router, b->moe_logits);
+    if (b->capture) cap_store(b, 7, il, b->moe_logits, n * ne); /* router logits, before the softmax */
     /* per-expert token lists */
     size_t *cnt = (size_t *)calloc(ne, sizeof(size_t));
     size_t *tok = (size_t *)malloc(ne * n * sizeof(size_t));
@@ -978,7 +979,7 @@ int or_forward(or_backend *b, const uint32_t *tokens, size_t n, size_t pos0, int
         if (b->capture) cap_store(b, 0, il, b->x, n * e);
 
         par_rmsnorm(b->pool, b->xn, b->x, L->ffn_norm, n, e, m->rms_eps);
-        if (L->is_moe) moe_ffn(b, &L->moe, b->xn, n, b->o);
+        if (L->is_moe) moe_ffn(b, &L->moe, b->xn, n, b->o, il);
         else {
             dense_ffn(b, &L->dense, b->xn, n, b->o);
             if (b->capture) cap_store(b, 6, il, b->gate, n * L->dense.gate.rows);

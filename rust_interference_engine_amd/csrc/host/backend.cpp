@@ -236,7 +236,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         d_moe_rows_ = dalloc<int>(allocs_, mb * nu);
         d_moe_rw_ = dalloc<float>(allocs_, mb * nu);
     }
-    cap_.resize(7);
+    cap_.resize(8);
     RIE_HIP_CHECK(hipDeviceSynchronize());
 }
 
@@ -280,22 +280,24 @@ void HipBackend::check_launch(const char *what) {
 
 // QuantActs::prepare (matmul.rs:34-71): quantize x (optionally RMS-normalized)
 // once per activation format the given weights consume.
-void HipBackend::prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32) {
+// ref_order: the norm sums in the reference's order (see launch_rmsnorm_quant).
+void HipBackend::prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32,
+                         bool ref_order) {
     bool need[3] = {want_f32, false, false};
     for (int i = 0; i < nw; i++)
         if (ws[i] && ws[i]->ty >= 0) need[act_format(ws[i]->ty)] = true;
     const float eps = m_.cfg.rms_eps;
     bool wrote_f32 = false;
     if (need[ACT_Q8_0]) {
-        launch_rmsnorm_quant(x, K, norm, eps, n, K, need[ACT_F32] ? d_xn_ : nullptr, ACT_Q8_0, act0_, st_);
+        launch_rmsnorm_quant(x, K, norm, eps, n, K, need[ACT_F32] ? d_xn_ : nullptr, ACT_Q8_0, act0_, st_, ref_order);
         wrote_f32 = need[ACT_F32];
     }
     if (need[ACT_Q8K]) {
-        launch_rmsnorm_quant(x, K, norm, eps, n, K, (need[ACT_F32] && !wrote_f32) ? d_xn_ : nullptr, ACT_Q8K, actk_, st_);
+        launch_rmsnorm_quant(x, K, norm, eps, n, K, (need[ACT_F32] && !wrote_f32) ? d_xn_ : nullptr, ACT_Q8K, actk_, st_, ref_order);
         wrote_f32 = wrote_f32 || need[ACT_F32];
     }
     if (need[ACT_F32] && !wrote_f32) {
-        if (norm) launch_rmsnorm(x, K, norm, eps, n, K, d_xn_, K, 0, st_);
+        if (norm) launch_rmsnorm(x, K, norm, eps, n, K, d_xn_, K, 0, st_, ref_order);
         else RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, x, (size_t)n * K * 4, hipMemcpyDeviceToDevice, st_));
     }
     check_launch("prepare");
@@ -368,16 +370,23 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
     for (size_t il = 0; il < c.n_layer; il++) {
         const DevLayer &L = layers_[il];
         const bool swa = c.is_swa(il);
+        cur_layer_ = il;
         // ---- attention block ----
         const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
         // single token with Q4_0/Q8_0 or K-quant Q/K/V of one activation format:
         // the GEMV normalizes and quantizes x itself
         const int qkv_fmt = act_format(L.wq.ty);
-        const bool self_norm = n == 1 && !capture_ && L.attn_norm && gemv_norm_ok(L.wq.ty, E) && gemv_norm_ok(L.wk.ty, E) &&
-                               gemv_norm_ok(L.wv.ty, E) && act_format(L.wk.ty) == qkv_fmt && act_format(L.wv.ty) == qkv_fmt;
+        // The first layer's input rows are the embedding rows, the same bits as the
+        // reference's: its norm sums in the reference's order (a standalone launch), so
+        // its activation codes are the reference's too.  Later layers' inputs already
+        // carry f32 reduction-order differences, and their norms use wide sums.
+        const bool first = il == 0;
+        const bool self_norm = n == 1 && !capture_ && !first && L.attn_norm && gemv_norm_ok(L.wq.ty, E) &&
+                               gemv_norm_ok(L.wk.ty, E) && gemv_norm_ok(L.wv.ty, E) && act_format(L.wk.ty) == qkv_fmt &&
+                               act_format(L.wv.ty) == qkv_fmt;
         const NormIn nin{d_x_, L.attn_norm, c.rms_eps};
         if (!self_norm) {
-            prepare(d_x_, L.attn_norm, n, E, ws, 3, false);
+            prepare(d_x_, L.attn_norm, n, E, ws, 3, false, first);
             mark("rmsnorm_quant");
         }
         GemvSeg qkv[3] = {{L.wq, d_q_, qd, EPI_STORE}, {L.wk, d_k_, kvd, EPI_STORE}, {L.wv, d_v_, kvd, EPI_STORE}};
@@ -596,6 +605,12 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
             throw rt_err("normalizing router GEMV launch failed");
     } else {
         matmul(&rs, 1, n, E);
+    }
+    if (capture_ && !in_capture_) {  // router logits before the softmax
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        cap_[7].resize(c.n_layer);
+        cap_[7][cur_layer_].resize((size_t)n * ne);
+        RIE_HIP_CHECK(hipMemcpy(cap_[7][cur_layer_].data(), d_router_, (size_t)n * ne * 4, hipMemcpyDeviceToHost));
     }
     launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
     check_launch("moe route");

@@ -88,7 +88,8 @@ class HipBackend {
     DevWeight dev(const HostWeight &w) const;
     const float *dev_vec(const HostWeight &w);
     void run_layers(int n, size_t pos0, const int *d_pos0, bool all_logits, int n_split);
-    void prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32);
+    void prepare(const float *x, const float *norm, int n, int K, const DevWeight *const *ws, int nw, bool want_f32,
+                 bool ref_order = false);
     void matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8 *act_q8_0 = nullptr);
     void ffn_dense(const DevLayer &L, int n, float *out_resid, int epi);
     // writes the block's output to d_o_, or (true returned) adds it to d_x_ itself
@@ -141,6 +142,7 @@ class HipBackend {
     std::vector<float> hidden_host_;
     bool capture_ = false;
     std::vector<std::vector<std::vector<float>>> cap_;  // [what][layer]
+    size_t cur_layer_ = 0;                               // layer run_layers is in (capture bookkeeping)
 
     // per-launch event marks while profiling (eager path only)
     void mark(const char *name);

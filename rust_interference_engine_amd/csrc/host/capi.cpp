@@ -231,7 +231,7 @@ int32_t rie_hip_k_rmsnorm_quant(const float *x, const float *w, float eps, int32
         a.s = s;
         a.isum = isum;
         a.bsums = bsums;
-        rie::launch_rmsnorm_quant(x, k, w, eps, n, k, xn, fmt, a, 0);
+        rie::launch_rmsnorm_quant(x, k, w, eps, n, k, xn, fmt, a, 0, true);
         RIE_HIP_CHECK(hipGetLastError());
         RIE_HIP_CHECK(hipDeviceSynchronize());
     });

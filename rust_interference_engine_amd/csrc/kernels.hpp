@@ -6,10 +6,13 @@
 namespace rie {
 
 // ---- quant.hip ----
+// ref_order: the norm's Σx² in the reference's summation order (kernels/avx2.rs:
+// dot_f32), bitwise the reference's normalized row for the same input row (a
+// serial sum: for rows that are identical on both sides, the first layer's).
 void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
-                          hipStream_t st);
+                          hipStream_t st, bool ref_order = false);
 void launch_rmsnorm(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *out, int ldo, int inplace_assoc,
-                    hipStream_t st);
+                    hipStream_t st, bool ref_order = false);
 void launch_embed(const uint32_t *tokens, int n, const DevWeight &table, float scale, float *x, hipStream_t st);
 
 // ---- gemv.hip ----

@@ -22,13 +22,14 @@ namespace rie {
 constexpr int Q8_0_BLOCKS_PER_WG = 16;
 constexpr int Q8K_BLOCKS_PER_WG = 4;
 
+// ref_order: the norm's sum of squares in the reference's order (sumsq_ref_order).
 template <int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w,
-                                                            float eps, int E, float *__restrict__ xn, ActQ8 act) {
+                                                            float eps, int E, float *__restrict__ xn, ActQ8 act, int ref_order) {
     __shared__ float red[4];
     const int row = blockIdx.y;
     const float *xr = x + (size_t)row * ldx;
-    const float scale = w ? rms_scale_wg(xr, E, eps, red) : 1.0f;
+    const float scale = w ? (ref_order ? rms_scale_ref_wg(xr, E, eps, red) : rms_scale_wg(xr, E, eps, red)) : 1.0f;
     if (FMT == ACT_Q8_0) {
         const int b0 = blockIdx.x * Q8_0_BLOCKS_PER_WG;
         quant_q8_0_range(xr, w, scale, E, xn, act, row, b0, min(E >> 5, b0 + Q8_0_BLOCKS_PER_WG));
@@ -43,12 +44,14 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restr
 // and every thread writes its 16 codes with one store.  With w, the row is first
 // reduced to its RMSNorm scale and then quantized (second read from L2).
 __global__ __launch_bounds__(256) void q8_0_rows_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w, float eps,
-                                                        int E, float *__restrict__ xn, ActQ8 act) {
+                                                        int E, float *__restrict__ xn, ActQ8 act, int ref_order) {
     __shared__ float red[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *xr = x + (size_t)row * ldx;
     float scale = 1.0f;
-    if (w) {
+    if (w && ref_order) {
+        scale = rms_scale_ref_wg(xr, E, eps, red);
+    } else if (w) {
         float ss = 0.0f;
         for (int i0 = 16 * tid; i0 < E; i0 += 4096)
 #pragma unroll
@@ -119,42 +122,48 @@ __global__ __launch_bounds__(256) void q8_0_rows_kernel(const float *__restrict_
 }
 
 void launch_rmsnorm_quant(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *xn, int fmt, const ActQ8 &act,
-                          hipStream_t st) {
+                          hipStream_t st, bool ref_order) {
+    const int ro = ref_order ? 1 : 0;
     if (fmt == ACT_Q8_0) {
         if (E % 32 == 0 && ldx % 4 == 0) {
-            hipLaunchKernelGGL(q8_0_rows_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+            hipLaunchKernelGGL(q8_0_rows_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act, ro);
             return;
         }
         const int chunks = (E / 32 + Q8_0_BLOCKS_PER_WG - 1) / Q8_0_BLOCKS_PER_WG;
-        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8_0>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act, ro);
     } else {
         const int chunks = (E / 256 + Q8K_BLOCKS_PER_WG - 1) / Q8K_BLOCKS_PER_WG;
-        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8K>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act);
+        hipLaunchKernelGGL(rmsnorm_quant_kernel<ACT_Q8K>, dim3(chunks, n_rows), dim3(256), 0, st, x, ldx, w, eps, E, xn, act, ro);
     }
 }
 
 // RMSNorm without quantization (f32 out), one row per workgroup: ops.rs:7-14
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w, float eps,
-                                                      int E, float *__restrict__ out, int ldo, int inplace_assoc) {
+                                                      int E, float *__restrict__ out, int ldo, int inplace_assoc, int ref_order) {
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *xr = x + (size_t)row * ldx;
     __shared__ float red[4];
     __shared__ float s_scale;
-    float ss = 0.0f;
-    for (int i = tid; i < E; i += 256) ss = fmaf(xr[i], xr[i], ss);
-    ss = wave_sum(ss, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    if (tid == 0) s_scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)E + eps);
-    __syncthreads();
-    const float scale = s_scale;
+    float scale;
+    if (ref_order) {
+        scale = rms_scale_ref_wg(xr, E, eps, red);
+    } else {
+        float ss = 0.0f;
+        for (int i = tid; i < E; i += 256) ss = fmaf(xr[i], xr[i], ss);
+        ss = wave_sum(ss, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) s_scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)E + eps);
+        __syncthreads();
+        scale = s_scale;
+    }
     float *o = out + (size_t)row * ldo;
     for (int i = tid; i < E; i += 256) o[i] = inplace_assoc ? xr[i] * (scale * w[i]) : xr[i] * scale * w[i];
 }
 
 void launch_rmsnorm(const float *x, int ldx, const float *w, float eps, int n_rows, int E, float *out, int ldo, int inplace_assoc,
-                    hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, out, ldo, inplace_assoc);
+                    hipStream_t st, bool ref_order) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, st, x, ldx, w, eps, E, out, ldo, inplace_assoc, ref_order ? 1 : 0);
 }
 
 // ---- token embedding: dequantize_row (quant/reference.rs:53-215) ---------------

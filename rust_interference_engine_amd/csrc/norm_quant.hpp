@@ -47,6 +47,57 @@ __device__ __forceinline__ float rms_scale_wg(const float *__restrict__ xr, int 
     return 1.0f / sqrtf(t / (float)E + eps);
 }
 
+// Σx² of a row summed in the order of the reference's x86 dot_f32
+// (kernels/avx2.rs:186-203, called by rmsnorm, ops.rs:7-14): lane L < 16 of the
+// calling wave accumulates x[16j+L]² with one fma per j, in j order (lanes 0-7
+// are the accumulator acc0, lanes 8-15 acc1); then acc0 + acc1 and the hsum_ps
+// tree ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)) as exchanges at lane offsets 8, 4,
+// 2, 1 (each addition the reference's, operands commuted at most); then the
+// sequential tail s + x[i]·x[i] (not fused) over the last E % 16 values.  For
+// the same row this is the reference's sum bit for bit.  Lanes 16-63 repeat
+// lanes 0-15; every lane returns the sum.  Serial: E/16 dependent fmas.
+template <bool COH = false>
+__device__ __forceinline__ float sumsq_ref_order(const float *__restrict__ xr, int E) {
+    const int L = threadIdx.x & 15;
+    const int nj = E >> 4;
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + 8 <= nj; j += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = ld_row<COH>(xr + 16 * (j + u) + L);
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = fmaf(v[u], v[u], acc);
+    }
+    for (; j < nj; j++) {
+        const float v = ld_row<COH>(xr + 16 * j + L);
+        acc = fmaf(v, v, acc);
+    }
+    acc = acc + xor_f<8>(acc);
+    acc = acc + xor_f<4>(acc);
+    acc = acc + xor_f<2>(acc);
+    acc = acc + xor_f<1>(acc);
+    float s = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+    for (int i = nj << 4; i < E; i++) {
+        const float v = ld_row<COH>(xr + i);
+        s = s + v * v;
+    }
+    return s;
+}
+
+// 1/√(Σx²/E + eps) with Σx² in the reference's order (sumsq_ref_order, by the
+// first wave), for a workgroup (red: 1 float of LDS).
+template <bool COH = false>
+__device__ __forceinline__ float rms_scale_ref_wg(const float *__restrict__ xr, int E, float eps, float *red) {
+    __syncthreads();  // red may still be read by a previous call
+    if (threadIdx.x < 64) {
+        const float ss = sumsq_ref_order<COH>(xr, E);
+        if (threadIdx.x == 0) red[0] = 1.0f / sqrtf(ss / (float)E + eps);
+    }
+    __syncthreads();
+    return red[0];
+}
+
 // Q8_0 blocks [blo, bhi) of row `row` (E values); y = w ? x·scale·w : x.
 template <bool COH = false>
 __device__ __forceinline__ void quant_q8_0_range(const float *__restrict__ xr, const float *__restrict__ w, float scale, int E,

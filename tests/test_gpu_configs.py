@@ -1,0 +1,326 @@
+"""Parity of the HIP path with the oracle at the shapes of the benchmark
+workloads: full widths, vocabularies and head types, with the layer count cut
+to what the CPU oracle finishes in seconds.
+
+  llama8b   Llama-3.1-8B shape, Q4_0, untied Q4_0 head (V 128256), f16 KV
+  qwen3_1b7 Qwen3-1.7B shape, Q4_0 layers, QK-norm, tied Q6_K head (V 151936)
+  llama3b   Llama-3.2-3B shape, Q4_K_M mix (Q6_K attn_v, Q4_K and Q6_K ffn_down), tied Q6_K head
+  qwen3moe  Qwen3-30B-A3B shape, 128 experts of FFN 768, top-8, Q4_K, F32 router
+
+Each runs a 512-token prompt as one batch (the int8 MFMA GEMMs at 128-token
+tiles, the prompt attention), compares every token's residual row after the
+last layer, then 64 teacher-forced decode steps through the replayed decode
+graph (the fused single-token kernels at contexts 512..575: 16 attention
+ranges), and finally 128 free-running greedy steps on both sides
+(Engine::bench semantics, engine.rs:540-564; argmax with the first maximum,
+sampler.rs:199-209).
+
+Per step: logits max-abs, max-rel (tests/common/mod.rs:33-36) and
+KL(softmax_cpu || softmax_gpu).  Bounds: max-rel below the reference's
+quantized whole-model tolerance 0.03 (tests/model.rs:340-375) and KL below
+1e-3 at every step.  The two sides sum f32 partial products in different
+orders, and every later activation quantizer turns those last-bit differences
+into whole-step code flips near its rounding boundaries, so the logits of a
+random-weight model with a 128K-152K vocabulary drift apart by about 1% within
+two layers, and routed-expert choices flip where two router logits nearly tie.
+Greedy agreement is therefore asserted outside near-ties: a teacher-forced
+step may pick another token only where the CPU's top-2 logit margin is within
+twice that step's largest logit difference, and the free-running sequences must
+be identical up to the first step whose CPU top-2 margin is within twice the
+largest logit difference seen.  The measured figures (and the count of
+identical free-running steps) are appended to gpurun_out/parity_records.jsonl
+when that directory can be written.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+import rust_interference_engine_amd as R  # noqa: E402
+from rust_interference_engine_amd import synth  # noqa: E402
+
+N_PROMPT, N_TF, N_FREE = 512, 64, 128
+
+
+def _spec(name):
+    if name == "llama8b":
+        s = synth.baseline_llama31_8b_q4_0()
+    elif name == "qwen3_1b7":
+        s = synth.baseline_qwen3_1_7b_q4_0()
+    elif name == "llama3b":
+        s = synth.baseline_llama32_3b_q4_k_m()
+    else:
+        s = synth.baseline_qwen3_30b_a3b_q4_k()
+    s.n_layer = 2
+    return s
+
+
+def _prompt(seed, n, nv):
+    """seeded uniform-random token ids: Rng::new(seed).next_u64() % V (testing.rs:10-30)"""
+    import pyoracle
+    r = pyoracle.Rng(seed)
+    return [int(r.next_u64() % nv) for _ in range(n)]
+
+
+def _softmax64(x):
+    x = x.astype(np.float64)
+    e = np.exp(x - x.max())
+    return e / e.sum()
+
+
+def logit_metrics(gpu, cpu):
+    p, q = _softmax64(cpu), _softmax64(gpu)
+    kl = float(np.sum(p * (np.log(np.maximum(p, 1e-300)) - np.log(np.maximum(q, 1e-300)))))
+    diff = np.abs(gpu.astype(np.float64) - cpu.astype(np.float64))
+    return {"max_abs": float(diff.max()), "max_rel": float(diff.max() / max(np.abs(cpu).max(), 1e-30)), "kl": kl}
+
+
+def _record(rec):
+    d = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
+    try:
+        os.makedirs(d, exist_ok=True)
+        with open(os.path.join(d, "parity_records.jsonl"), "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    except OSError:
+        pass
+
+
+def _top2(x):
+    a = np.partition(x, -2)[-2:]
+    return float(a[1] - a[0])
+
+
+def _routing_flips(gr, orr, k):
+    """Per token: does the GPU's top-k expert set (router logits gr, ties to the
+    lower index, cpu.rs:495) differ from the CPU's, and if so is it at a near-tie
+    (the CPU's k-th minus (k+1)-th logit within twice the largest router logit
+    difference)?  Returns (differs, excused) boolean arrays."""
+    n = orr.shape[0]
+    differs, excused = np.zeros(n, bool), np.zeros(n, bool)
+    for t in range(n):
+        ids = np.arange(orr.shape[1])
+        sg = set(np.lexsort((ids, -gr[t]))[:k].tolist())
+        so = np.lexsort((ids, -orr[t]))
+        if sg != set(so[:k].tolist()):
+            differs[t] = True
+            margin = float(orr[t, so[k - 1]] - orr[t, so[k]])
+            excused[t] = margin <= 2 * float(np.abs(gr[t] - orr[t]).max())
+    return differs, excused
+
+
+def _routing_explains(g, o, L, n, ne, k, rows, row_err):
+    """rows (token indices of the last forward) whose result is off by row_err
+    (relative): True when each of them, in some layer, took a different expert
+    set than the CPU at a router near-tie, or kept the set but had its
+    combination weights (softmax over the top k, renormalized, cpu.rs:496-501)
+    moved by at least a quarter of its error.  Router logits of N(0, 1) gate
+    weights have a standard deviation of √E (45 at E 2048), so the last-bit
+    drift of x moves them by tenths and the weights by tens of percent."""
+    explained = np.zeros(n, bool)
+    for il in range(L):
+        gr, orr = g.capture(il, 7, n * ne).reshape(n, ne), o.capture(il, 7).reshape(n, ne)
+        d, ex = _routing_flips(gr, orr, k)
+        assert np.all(ex[d]), f"layer {il}: expert choice differs without a router near-tie at tokens {np.where(d & ~ex)[0]}"
+        explained |= d
+        for t, err in zip(rows, row_err):
+            if d[t]:
+                continue
+            sel = np.lexsort((np.arange(ne), -orr[t]))[:k]
+            wg = np.exp(gr[t, sel].astype(np.float64) - gr[t, sel].max())
+            wo = np.exp(orr[t, sel].astype(np.float64) - orr[t, sel].max())
+            if np.abs(wg / wg.sum() - wo / wo.sum()).max() >= err / 4:
+                explained[t] = True
+    return bool(np.all(explained[rows]))
+
+
+@pytest.mark.parametrize("name", ["llama8b", "qwen3_1b7", "llama3b", "qwen3moe"])
+def test_workload_shape_matches_oracle(oracle, name):
+    assert torch.cuda.is_available(), "needs the MI355X"
+    spec = _spec(name)
+    img = synth.build(spec)
+    nv, E, L = spec.n_vocab, spec.n_embd, spec.n_layer
+    n_ctx = N_PROMPT + N_FREE + 64
+    g = R.HipBackend(img, n_ctx=n_ctx, max_batch=N_PROMPT)
+    o = oracle.Backend(oracle.Model(img), n_ctx, N_PROMPT, 0, n_threads=min(16, os.cpu_count() or 1))
+    prompt = _prompt(7, N_PROMPT, nv)
+    print(f"{name}: prompt of {N_PROMPT} as one batch", flush=True)
+
+    # ---- the prompt: every token's residual row after the last layer, and the last logits
+    g.set_capture(True)
+    o.set_capture(True)
+    lg = g.forward(prompt, 0)
+    lo = o.forward(prompt, 0)
+    xg = g.capture(L - 1, 1, N_PROMPT * E).reshape(N_PROMPT, E)
+    xo = o.capture(L - 1, 1).reshape(N_PROMPT, E)
+    row_rel = np.abs(xg - xo).max(axis=1) / np.abs(xo).max(axis=1)
+    off = np.where(row_rel >= 0.05)[0]
+    explained = bool(spec.n_expert and off.size and
+                     _routing_explains(g, o, L, N_PROMPT, spec.n_expert, spec.n_expert_used, off, row_rel[off]))
+    g.set_capture(False)
+    o.set_capture(False)
+    m0 = logit_metrics(lg, lo)
+    rec = {"config": name, "layers": L, "hidden": E, "vocab": nv, "prompt_rows_max_rel": float(row_rel.max()),
+           "prompt_rows_median_rel": float(np.median(row_rel)), "prompt_rows_over_0.03": int((row_rel >= 0.03).sum()),
+           "prompt_logits": m0}
+    print(f"{name}: {rec}", flush=True)
+    # residual rows after the last layer: the same drift as the logits, per token; with
+    # experts, a token whose top-k flipped on a router near-tie (checked) takes other experts
+    assert np.median(row_rel) < 0.02, rec
+    assert off.size == 0 or explained, f"{name}: prompt rows {off} off by up to {row_rel.max()} without an expert-choice flip"
+    assert m0["max_rel"] < 0.03 and m0["kl"] < 1e-3, (name, m0)
+
+    # ---- teacher-forced decode through the replayed graph: the CPU's token each step
+    tf, agree, bad = [], 0, []
+    for step in range(N_TF):
+        tok = oracle.argmax(lo)
+        if R.argmax(lg) == tok:
+            agree += 1
+        else:
+            bad.append((step, _top2(lo), float(np.abs(lg - lo).max())))
+        pos = N_PROMPT + step
+        lg, lo = g.forward([tok], pos), o.forward([tok], pos)
+        m = logit_metrics(lg, lo)
+        m["routing_flip"] = False
+        if spec.n_expert and (m["max_rel"] >= 0.03 or m["kl"] >= 1e-3):
+            # the same step again with the router logits captured (the same cache rows are
+            # rewritten with the same bits; capture mode's logits equal the graph's bitwise)
+            g.set_capture(True)
+            o.set_capture(True)
+            lg2, lo2 = g.forward([tok], pos), o.forward([tok], pos)
+            assert np.array_equal(lo2, lo) and np.array_equal(lg2, lg), "step not reproducible"
+            m["routing_flip"] = _routing_explains(g, o, L, 1, spec.n_expert, spec.n_expert_used, [0],
+                                                  [max(m["max_rel"], 0.03)])
+            g.set_capture(False)
+            o.set_capture(False)
+        tf.append(m)
+    plain = [m for m in tf if not m["routing_flip"]]  # steps whose expert weights moved are excused
+    rec["decode_max_rel"] = max(m["max_rel"] for m in plain)
+    rec["decode_max_abs"] = max(m["max_abs"] for m in plain)
+    rec["decode_max_kl"] = max(m["kl"] for m in plain)
+    rec["decode_median_kl"] = float(np.median([m["kl"] for m in tf]))
+    rec["decode_steps_with_expert_flip"] = [i for i, m in enumerate(tf) if m["routing_flip"]]
+    rec["teacher_forced_argmax_agree"] = f"{agree}/{N_TF}"
+    rec["teacher_forced_disagreements"] = [(i, round(mg, 5), round(d, 5)) for i, mg, d in bad]
+    print(f"{name}: {rec}", flush=True)
+    assert rec["decode_max_rel"] < 0.03 and rec["decode_max_kl"] < 1e-3, rec
+    for i, mg, d in bad:  # a different choice only inside the noise band (or after an expert flip)
+        assert mg <= 2 * d or (i > 0 and tf[i - 1]["routing_flip"]), \
+            f"{name}: teacher-forced step {i}: cpu margin {mg} exceeds 2x logit difference {d}"
+
+    # ---- 128 free-running greedy steps on both sides
+    want, margins, _ = o.greedy(prompt, N_FREE, N_PROMPT)
+    first = g.forward_argmax(prompt, 0)
+    got = g.generate_greedy(N_PROMPT, N_FREE)
+    assert int(got[0]) == first
+    noise = max([m0["max_abs"]] + [m["max_abs"] for m in tf])
+    diverge = next((i for i in range(N_FREE) if int(got[i]) != int(want[i])), None)
+    near_tie = next((i for i in range(N_FREE) if margins[i] <= 2 * noise), None)
+    rec["greedy_steps_identical"] = N_FREE if diverge is None else diverge
+    rec["greedy_first_near_tie"] = near_tie
+    if diverge is not None:
+        rec["divergence_top2_margin"] = float(margins[diverge])
+    _record(rec)
+    print(f"{name}: {rec}", flush=True)
+    if diverge is not None:
+        assert near_tie is not None and diverge >= near_tie, \
+            f"{name}: greedy sequences differ from step {diverge} (cpu top-2 margin {margins[diverge]}, noise {noise})"
+    g.close()
+
+
+LEVELS_I8 = np.array([-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126], np.float64)  # turbo.rs:126
+
+
+def _turbo_rows(rows, scales, hd):
+    """codes (Q4_0 nibble order, turbo.rs:157) and f16 scales -> rotated-domain values scale·level/46"""
+    lo, hi = rows & 0xF, rows >> 4
+    codes = np.empty(rows.shape[:-1] + (hd,), np.int64)
+    for c in range(hd // 32):
+        codes[..., 32 * c:32 * c + 16] = lo[..., 16 * c:16 * c + 16]
+        codes[..., 32 * c + 16:32 * c + 32] = hi[..., 16 * c:16 * c + 16]
+    sc = scales.view(np.float16).astype(np.float64)
+    return codes, sc
+
+
+@pytest.mark.parametrize("kv", [0, 2], ids=["f16", "turbo4"])
+def test_long_context_attention(oracle, kv):
+    """The 32K-context workload on one layer of the Llama-3.1-8B shape: a
+    32768-token prompt in batches of 512 (Engine::eval_tokens chunking), then
+    single-token steps at positions 32768..32770, where decode attention runs 64
+    context ranges of 513 positions.  KV codes bit-exact against the reference
+    encoders on the GPU's own K/V rows at sampled batches (f16 RNE; Turbo4
+    quantize_4, turbo.rs:166-171); the decode attention output against float64
+    on the captured query and the whole cache: for f16 the f32 bound of the
+    short-context test, for Turbo4 the reference's rotated-domain arithmetic
+    (query rotated and quantized to Q8_0 as cpu.rs:584-600 does, integer level
+    dots per 32-value chunk, dot_rotated_4 turbo.rs:178-193; weighted sum of
+    levels and the inverse rotation, turbo.rs:222-250, cpu.rs:630-632)."""
+    assert torch.cuda.is_available(), "needs the MI355X"
+    n_prompt, mb = 32768, 512
+    spec = synth.baseline_llama31_8b_q4_0(ctx=n_prompt + 256)
+    spec.n_layer = 1
+    img = synth.build(spec)
+    nv, hd, nh, nkv = spec.n_vocab, spec.head_dim, spec.n_head, spec.n_head_kv
+    n_ctx = n_prompt + 64
+    g = R.HipBackend(img, n_ctx=n_ctx, max_batch=mb, kv_type=kv)
+    prompt = _prompt(11, n_prompt + 3, nv)
+    sampled = {0, 31 * mb, n_prompt - mb}
+    for p0 in range(0, n_prompt, mb):
+        cap = p0 in sampled
+        g.set_capture(cap)
+        g.forward(prompt[p0:p0 + mb], p0)
+        if not cap:
+            continue
+        print(f"kv{kv}: checking cache rows of positions {p0}..{p0 + mb - 1}", flush=True)
+        for which, what in ((0, 4), (1, 5)):
+            src = g.capture(0, what, mb * nkv * hd).reshape(mb, nkv, hd)
+            rows, scales = g.kv_layer(0, which, nkv, n_ctx)
+            for t in range(0, mb, 37):
+                for h in range(nkv):
+                    if kv == 0:
+                        assert np.array_equal(rows[h, p0 + t], src[t, h].astype(np.float16).view(np.uint8)), (p0 + t, h)
+                    else:
+                        ref = oracle.turbo_quantize(src[t, h])
+                        assert np.array_equal(rows[h, p0 + t], ref[2:]), (p0 + t, h)
+                        assert scales[h, p0 + t] == ref[:2].view(np.uint16)[0], (p0 + t, h)
+    g.set_capture(True)
+    G = nh // nkv
+    worst = 0.0
+    for p in range(n_prompt, n_prompt + 3):
+        g.forward([prompt[p]], p)
+        q = g.capture(0, 3, nh * hd).reshape(nh, hd)
+        att = g.capture(0, 2, nh * hd).reshape(nh, hd)
+        kr, ks = g.kv_layer(0, 0, nkv, n_ctx)
+        vr, vs = g.kv_layer(0, 1, nkv, n_ctx)
+        n = p + 1
+        for hq in range(nh):
+            h = hq // G
+            if kv == 0:
+                K = kr[h, :n].view(np.float16).astype(np.float64).reshape(n, hd)
+                V = vr[h, :n].view(np.float16).astype(np.float64).reshape(n, hd)
+                s = K @ q[hq].astype(np.float64)
+                w = np.exp(s - s.max())
+                ref = (w / w.sum()) @ V
+                bound = (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * np.abs(V).max() + 1e-6
+            else:
+                kc, ksc = _turbo_rows(kr[h, :n], ks[h, :n], hd)
+                vc, vsc = _turbo_rows(vr[h, :n], vs[h, :n], hd)
+                qa = oracle.quantize_q8_0(oracle.turbo_rotate(q[hq]))  # [hd/32] blocks: qs[32], d
+                qs = qa["qs"].reshape(-1).astype(np.float64)
+                dq = qa["d"].astype(np.float64)
+                idots = (LEVELS_I8[kc] * qs).reshape(n, hd // 32, 32).sum(axis=2)  # exact integers per chunk
+                s = (idots * dq).sum(axis=1) * ksc / 46.0
+                w = np.exp(s - s.max())
+                orot = ((w / w.sum() * vsc)[:, None] * LEVELS_I8[vc] / 46.0).sum(axis=0)
+                ref = oracle.turbo_rotate(orot.astype(np.float32), inverse=True).astype(np.float64)
+                vmax = np.abs(vsc[:, None] * LEVELS_I8[vc] / 46.0).max()
+                bound = (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * vmax + 2e-6 * vmax + 1e-6
+            err = float(np.abs(att[hq] - ref).max())
+            worst = max(worst, err / bound)
+            assert err <= bound, f"kv{kv} position {p} head {hq}: {err} > {bound}"
+    _record({"config": "llama8b_32k_1layer", "kv": ["f16", "q8_0", "turbo4"][kv], "context": n_prompt + 3,
+             "decode_attention_err_over_bound": worst})
+    g.close()

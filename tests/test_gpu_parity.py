@@ -103,19 +103,33 @@ def test_q8_k_activation_codes_bit_exact(oracle, cuda):
             assert np.array_equal(g["bsums"][t * k // 16:(t + 1) * k // 16], ref["bsums"].reshape(-1))
 
 
-def test_rmsnorm_then_quant(oracle, cuda):
-    """normalized rows within f32 rounding of ops.rs:7-14; codes bit-exact on the GPU's own rows"""
-    rng = np.random.default_rng(2)
-    n, k = 4, 4096
+@pytest.mark.parametrize("k", [256, 2048, 4096, 14336, 4128])
+def test_rmsnorm_then_quant_bitwise(oracle, cuda, k):
+    """RMSNorm with the reference's summation order (ops.rs:7-14 over kernels/
+    avx2.rs:186-203; 4128 leaves a partial 8-step group) then Q8_0 / Q8_K: the
+    normalized rows, codes and scales equal the oracle's bit for bit on the
+    same input rows.  Rows of dequantized Q4_0 weights (the first layer's input
+    in a Q4_0 model) put many values on exact quantizer ties, where a
+    reduction-order difference of one ulp in the norm would flip codes."""
+    rng = np.random.default_rng(2 + k)
+    n = 4
     x = rng.standard_normal((n, k)).astype(np.float32)
-    w = (1 + 0.1 * rng.uniform(-1, 1, k)).astype(np.float32)
-    g = _quant_on_gpu(x, 1, cuda, w=w)
-    L = oracle.lib()
-    for t in range(n):
-        ref = np.zeros(k, np.float32)
-        L.or_rmsnorm(oracle.ptr(ref), oracle.ptr(np.ascontiguousarray(x[t])), oracle.ptr(w), k, 1e-6)
-        assert np.abs(g["xn"][t] - ref).max() <= 4e-7 * np.abs(ref).max()
-        assert np.array_equal(g["qs"][t], oracle.quantize_q8_0(g["xn"][t])["qs"].reshape(-1))
+    blk = (np.round(rng.standard_normal((n, k)) * 3).clip(-8, 7) * 0.0123).astype(np.float32)  # Q4_0-like rows
+    x[n // 2:] = blk[n // 2:]
+    for w in ((1 + 0.1 * rng.uniform(-1, 1, k)).astype(np.float32), np.ones(k, np.float32)):
+        L = oracle.lib()
+        for fmt in (1, 2):
+            if fmt == 2 and k % 256:
+                continue
+            g = _quant_on_gpu(x, fmt, cuda, w=w)
+            for t in range(n):
+                ref = np.zeros(k, np.float32)
+                L.or_rmsnorm(oracle.ptr(ref), oracle.ptr(np.ascontiguousarray(x[t])), oracle.ptr(w), k, 1e-6)
+                assert np.array_equal(g["xn"][t].view(np.uint32), ref.view(np.uint32)), (k, fmt, t)
+                q = oracle.quantize_q8_0(ref) if fmt == 1 else oracle.quantize_q8_k(ref)
+                assert np.array_equal(g["qs"][t], q["qs"].reshape(-1)), (k, fmt, t)
+                nb = k // 32 if fmt == 1 else k // 256
+                assert np.array_equal(g["d"][t * nb:(t + 1) * nb].view(np.uint32), q["d"].view(np.uint32)), (k, fmt, t)
 
 
 def _gemv(ty, w, rows, k, act, act_f32, n_tok, cuda, gemm=False):
@@ -302,7 +316,21 @@ def test_prompt_batches_through_gemm_match_oracle(oracle, cuda, arch, ty):
 MOE_CASES = [  # (arch, weight type, tolerance, mutate): routed experts, shared expert + sigmoid gate, Q8_0 and Q8_K experts
     ("qwen3moe", F16, 3e-3, None), ("qwen2moe", F16, 3e-3, None), ("qwen3moe", Q4_K, 0.03, None),
     ("qwen3moe", Q4_0, 0.03, None), ("llama", Q8_0, 0.03, "mixtral"),
+    # a shared expert wider than the hidden size and the routed experts (scratch sized over it)
+    ("qwen2moe", F16, 3e-3, "wide_shared"), ("qwen2moe", Q4_K, 0.03, "wide_shared"),
+    # expert_used_count 0: the layers route to one expert (model/mod.rs:176)
+    ("qwen3moe", Q4_K, 0.03, "zero_used"),
+    # 128 experts, top-8, expert FFN 768 at hidden 1024 (the Qwen3-30B-A3B routing and widths)
+    ("qwen3moe", Q4_K, 0.03, "a3b"),
 ]
+MOE_MUTATIONS = {
+    None: None,
+    "mixtral": lambda s: [setattr(s, k, v) for k, v in (("n_expert", 4), ("n_expert_used", 2), ("n_ff_exp", 512))],
+    "wide_shared": lambda s: setattr(s, "n_ff_shexp", 1024),
+    "zero_used": lambda s: setattr(s, "n_expert_used", 0),
+    "a3b": lambda s: [setattr(s, k, v) for k, v in (("n_expert", 128), ("n_expert_used", 8), ("n_ff_exp", 768),
+                                                     ("n_embd", 1024))],
+}
 
 
 @pytest.mark.parametrize("arch,ty,tol,mut", MOE_CASES)
@@ -312,9 +340,7 @@ def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
     replay) against the oracle."""
     from naive_model import max_rel_err
 
-    def mixtral(s):
-        s.n_expert, s.n_expert_used, s.n_ff_exp = 4, 2, 512
-    spec, g, o = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16, mutate=mixtral if mut == "mixtral" else None)
+    spec, g, o = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16, mutate=MOE_MUTATIONS[mut])
     nv = spec.n_vocab
     toks = [(i * 41 + 7) % nv for i in range(20)]
     lg = g.forward(toks[:16], 0, True)
@@ -327,14 +353,26 @@ def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
         assert err < tol, f"{arch} {ty}: decode token {t}: {err}"
 
 
-@pytest.mark.parametrize("arch,ty", [("qwen3moe", Q4_K), ("qwen3moe", Q4_0), ("llama", Q4_0), ("llama", Q4_K)])
-def test_decode_prologues_equal_standalone_norm(oracle, cuda, arch, ty):
+PROLOGUE_WIDTHS = {  # hidden sizes past one superblock / one 4096-value pass, and the 768-wide expert FFN
+    None: None,
+    "e2048_ff768": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 2048), ("n_ff_exp", 768), ("n_ff", 1536))],
+    "e4096": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 4096), ("n_ff", 1024), ("n_ff_exp", 768))],
+}
+
+
+@pytest.mark.parametrize("arch,ty,width", [("qwen3moe", Q4_K, None), ("qwen3moe", Q4_0, None), ("llama", Q4_0, None),
+                                           ("llama", Q4_K, None), ("qwen3moe", Q4_K, "e2048_ff768"),
+                                           ("qwen3moe", Q4_0, "e2048_ff768"), ("llama", Q4_0, "e4096"),
+                                           ("llama", Q4_K, "e4096"), ("llama", Q4_K, "e2048_ff768")])
+def test_decode_prologues_equal_standalone_norm(oracle, cuda, arch, ty, width):
     """One-token decode normalizes x inside the GEMVs that read it: Q/K/V and
     gate/up (activation codes), and for MoE layers the router (f32 rows) and the
-    experts' gate/up; capture mode runs the standalone RMSNorm launches instead.
-    Decoding the same tokens at the same positions both ways gives bitwise
-    equal logits."""
-    spec, g, _ = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16)
+    experts' gate/up and down (the hidden's Q8_K); capture mode runs the
+    standalone RMSNorm and quantizer launches instead.  Decoding the same tokens
+    at the same positions both ways gives bitwise equal logits, at hidden sizes
+    from one superblock to 4096 (several superblocks and 4096-value passes per
+    workgroup) and at the 768-wide expert FFN."""
+    spec, g, _ = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16, mutate=PROLOGUE_WIDTHS[width])
     toks = [(i * 41 + 7) % spec.n_vocab for i in range(20)]
     g.forward(toks[:16], 0)
     fused = [np.array(g.forward([toks[t]], t)) for t in range(16, 20)]
