@@ -187,8 +187,10 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
                                 (int)((q.w >> sh) & 0x0F0F0F0Fu)};
                 const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, zi, 0, 0, 0);
                 const int sc = S.wsc[a][wrow * 8 + 4 * hs + j];
+                // 24-bit multiplies (|sc| < 64, |I| < 2^16): full-rate v_mad_i32_i24, where a
+                // 32-bit product would be the quarter-rate v_mul_lo_u32
 #pragma unroll
-                for (int v = 0; v < 16; v++) s1[a][v] += sc * I[v];
+                for (int v = 0; v < 16; v++) s1[a][v] += __mul24(sc, I[v]);
             }
         }
         if (hs == 1) {  // end of the superblock: the min term and the two scale products
