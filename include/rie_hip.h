@@ -166,7 +166,9 @@ int32_t rie_hip_time_ffn_glu(rie_hip_backend *b, int32_t reps, double *avg_us, s
  * Q8_0: qs [n][k], d/s/isum [n][k/32]; Q8_K: qs [n][k], d [n][k/256], bsums [n][k/16]. */
 int32_t rie_hip_k_rmsnorm_quant(const float *x, const float *w, float eps, int32_t n, int32_t k, int32_t fmt, float *xn, int8_t *qs,
                                 float *d, float *s, int32_t *isum, int16_t *bsums);
-/* out[t*rows + r] = W[r] · act[t] for one ggml weight matrix (kernels/mod.rs:136-232). */
+/* out[t*rows + r] = W[r] · act[t] for one ggml weight matrix (kernels/mod.rs:136-232).
+ * The kernels read whole aligned words around each block, so w must stay readable
+ * for 4096 bytes past its last row (the backend's weight upload keeps that slack). */
 int32_t rie_hip_k_gemv(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, const int8_t *qs, const float *d, const float *s,
                        const int32_t *isum, const int16_t *bsums, const float *act_f32, int32_t n_tok, float *out);
 /* the int8 MFMA prompt GEMM on the same operands (n_tok > 8) */

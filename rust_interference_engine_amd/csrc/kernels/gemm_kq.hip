@@ -19,6 +19,13 @@
 // Operand lane layout as in gemm.hip: lane l supplies row l mod 32 and values
 // 16·(l/32)..+16; tokens are permuted onto the A rows so that lane l's 16
 // results are the 16 consecutive tokens 16·(l/32) + v.
+//
+// Q6_K weights × Q8_K activations (kernels/avx2.rs dot_q6_k 109-151): per
+// superblock y += (f16(d_r)·d_t)·Σ_k sc_k·Σ_{16} (q6−32)·q8.  The codes are
+// unpacked once per stage into int8 q6−32 in LDS (four at a time); each
+// 16-value sub-block dot is one v_mfma_i32_32x32x16_i8 (exact), Σ_k sc_k·D_k
+// accumulates in int32 with 24-bit multiply-adds (|.| < 2^27), and the
+// superblock's float product is the rank-1 f32 MFMA of d_t and d_r.
 #include "../common.hpp"
 #include "../device.hpp"
 #include "../kernels.hpp"
@@ -137,6 +144,13 @@ __device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs 
     }
 }
 
+// c + a·b for |a|, |b| < 2^23 on the full-rate 24-bit multiplier (v_mul_i32_i24,
+// folded into v_mad_i32_i24 where the compiler can); a 32-bit product would be the
+// quarter-rate v_mul_lo_u32.  Plain code, not inline asm: b is an MFMA result, and
+// the compiler inserts the wait states between an MFMA and a VALU read of its
+// result only for instructions it generates itself.
+__device__ __forceinline__ int mad24(int a, int b, int c) { return c + __mul24(a, b); }
+
 template <bool GLU>
 __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     constexpr int NW = GLU ? 2 : 1;
@@ -186,11 +200,9 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
                 const v4i bw = {(int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu), (int)((q.z >> sh) & 0x0F0F0F0Fu),
                                 (int)((q.w >> sh) & 0x0F0F0F0Fu)};
                 const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, zi, 0, 0, 0);
-                const int sc = S.wsc[a][wrow * 8 + 4 * hs + j];
-                // 24-bit multiplies (|sc| < 64, |I| < 2^16): full-rate v_mad_i32_i24, where a
-                // 32-bit product would be the quarter-rate v_mul_lo_u32
+                const int sc = S.wsc[a][wrow * 8 + 4 * hs + j];  // |sc| < 64, |I| < 2^16
 #pragma unroll
-                for (int v = 0; v < 16; v++) s1[a][v] += __mul24(sc, I[v]);
+                for (int v = 0; v < 16; v++) s1[a][v] = mad24(sc, I[v], s1[a][v]);
             }
         }
         if (hs == 1) {  // end of the superblock: the min term and the two scale products
@@ -232,6 +244,164 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     }
 }
 
+// ---- Q6_K ----------------------------------------------------------------
+constexpr int K6_ST = 128 + 16;  // weight code bytes per row in LDS (one half superblock, padded)
+
+struct __align__(16) K6Stage {
+    int8_t a[KQ_BN * KA_ST];
+    float da[KQ_BN];
+    int8_t wq[KQ_BM * K6_ST];  // q6 − 32 of the half, in value order
+    float wd[KQ_BM];
+    int wsc[KQ_BM * 8];        // the half's 8 signed sub-block scales
+};
+
+struct K6Regs {
+    v4i a[2];
+    float da;
+    uint32_t lo[3], hi[3], qh[3];  // 8 bytes each from a 2-byte aligned address (+1 dword)
+    uint32_t sc[3];                // the half's 8 scale bytes
+    uint32_t d;
+    uint32_t sh_l, sh_h, sh_q, sh_s;
+};
+
+// 3 dwords from the dword-aligned address at or below p; sh = p's offset in the first
+__device__ __forceinline__ void ld3_a2(const uint8_t *p, uint32_t (&w)[3], uint32_t &sh) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t *q = (const uint32_t *)(a & ~(uintptr_t)3);
+    sh = (uint32_t)(a & 3);
+#pragma unroll
+    for (int i = 0; i < 3; i++) w[i] = wload(q + i);
+}
+
+// thread → (row tid/4, part tid%4): values l + 32i of the half, l in 8·part..+8, i = 0..3
+__device__ __forceinline__ void k6_load(const KqP &p, int sg, int row0, int t0, int sb, int hs, int tid, K6Regs &R) {
+    const int K = p.K, nsb = K >> 8;
+    {
+        const int tok = min(t0 + (tid >> 2), p.n_tok - 1);
+        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 256 * sb + 128 * hs + 32 * (tid & 3));
+        R.a[0] = src[0];
+        R.a[1] = src[1];
+    }
+    if (tid < KQ_BN) R.da = p.d[(size_t)min(t0 + tid, p.n_tok - 1) * nsb + sb];
+    const int row = min(row0 + (tid >> 2), p.rows[sg] - 1), part = tid & 3;
+    const uint8_t *blk = p.w[sg] + (size_t)row * p.rb[sg] + 210 * (size_t)sb;
+    ld3_a2(blk + 64 * hs + 8 * part, R.lo, R.sh_l);
+    ld3_a2(blk + 64 * hs + 32 + 8 * part, R.hi, R.sh_h);
+    ld3_a2(blk + 128 + 32 * hs + 8 * part, R.qh, R.sh_q);
+    if (part == 0) {
+        ld3_a2(blk + 192 + 8 * hs, R.sc, R.sh_s);
+        R.d = wload((const uint16_t *)(blk + 208));
+    }
+}
+
+__device__ __forceinline__ void k6_store(K6Stage &S, int tid, const K6Regs &R) {
+    {
+        v4i *dst = (v4i *)(S.a + (tid >> 2) * KA_ST + 32 * (tid & 3));
+        dst[0] = R.a[0];
+        dst[1] = R.a[1];
+    }
+    if (tid < KQ_BN) S.da[tid] = R.da;
+    const int row = tid >> 2, part = tid & 3;
+    const uint32_t lo[2] = {__builtin_amdgcn_alignbyte(R.lo[1], R.lo[0], R.sh_l), __builtin_amdgcn_alignbyte(R.lo[2], R.lo[1], R.sh_l)};
+    const uint32_t hi[2] = {__builtin_amdgcn_alignbyte(R.hi[1], R.hi[0], R.sh_h), __builtin_amdgcn_alignbyte(R.hi[2], R.hi[1], R.sh_h)};
+    const uint32_t qh[2] = {__builtin_amdgcn_alignbyte(R.qh[1], R.qh[0], R.sh_q), __builtin_amdgcn_alignbyte(R.qh[2], R.qh[1], R.sh_q)};
+    // value l + 32i: low nibble of ql[l] (i = 0), ql[l + 32] (i = 1), high nibbles (i = 2, 3);
+    // bits 2i, 2i+1 of qh[l] on top (quant/reference.rs:190-212).  Four codes per dword:
+    // (q | 0x80) − 32, then bit 7 flipped back, is the int8 q − 32 without cross-byte borrows.
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t *src = (i & 1) ? hi : lo;
+        const int sl = 4 * (i >> 1), sq = 2 * i;
+        uint32_t w[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t q = ((src[k] >> sl) & 0x0F0F0F0Fu) | (((qh[k] >> sq) & 0x03030303u) << 4);
+            w[k] = ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+        }
+        *(uint2 *)(S.wq + row * K6_ST + 32 * i + 8 * part) = make_uint2(w[0], w[1]);
+    }
+    if (part == 0) {
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(R.sc[1], R.sc[0], R.sh_s), s1 = __builtin_amdgcn_alignbyte(R.sc[2], R.sc[1], R.sh_s);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            S.wsc[row * 8 + k] = (int)(int8_t)(s0 >> (8 * k));
+            S.wsc[row * 8 + 4 + k] = (int)(int8_t)(s1 >> (8 * k));
+        }
+        S.wd[row] = h2f(R.d);
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
+    __shared__ K6Stage st[2];
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+    const int wr = wv >> 1, wc = wv & 1;
+    const int bid = blockIdx.x;  // workgroups of one row group share an XCD (id mod 8)
+    const int xcd = bid & 7, u = bid >> 3;
+    const int tg = u % p.n_tg;
+    const int rg = (u / p.n_tg) * 8 + xcd;
+    if (rg >= p.n_rg) return;  // whole workgroup: uniform
+    const int sg = (p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
+    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
+    const int t0 = tg * KQ_BN;
+    const int h = l >> 5, m = l & 31;
+    const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+    const int wrow = wr * 32 + m;
+    const int arow = wc * 32 + tok_m;
+    const v16i zi = {0};
+    const v16f zf = {0};
+    float acc[16];
+    int s1[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        acc[v] = 0.0f;
+        s1[v] = 0;
+    }
+    const int n_stages = (p.K >> 8) * 2;
+    K6Regs R;
+    k6_load(p, sg, row0, t0, 0, 0, tid, R);
+    k6_store(st[0], tid, R);
+    __syncthreads();
+    for (int s = 0; s < n_stages; s++) {
+        const int hs = s & 1;
+        if (s + 1 < n_stages) k6_load(p, sg, row0, t0, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        const K6Stage &S = st[s & 1];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {  // 16-value sub-blocks of the half
+            const long av = *(const long *)(S.a + arow * KA_ST + 16 * k + 8 * h);
+            const long bw = *(const long *)(S.wq + wrow * K6_ST + 16 * k + 8 * h);
+            const v16i D = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bw, zi, 0, 0, 0);
+            const int sc = S.wsc[wrow * 8 + k];
+#pragma unroll
+            for (int v = 0; v < 16; v++) s1[v] = mad24(sc, D[v], s1[v]);
+        }
+        if (hs == 1) {  // end of the superblock: (d_r·d_t)·Σ sc·D
+            const v16f p1 = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? S.da[arow] : 0.0f, h == 0 ? S.wd[wrow] : 0.0f, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                acc[v] = fmaf(p1[v], (float)s1[v], acc[v]);
+                s1[v] = 0;
+            }
+        }
+        if (s + 1 < n_stages) k6_store(st[(s + 1) & 1], tid, R);
+        __syncthreads();
+    }
+    const int rows = p.rows[sg];
+    const int row = row0 + wrow;
+    if (row >= rows) return;
+    float *out = p.out[sg];
+    const int ld = p.ld[sg];
+    const int epi = p.epi[sg];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int tok = t0 + wc * 32 + 16 * h + v;
+        if (tok < p.n_tok) {
+            float *o = out + (size_t)tok * ld + row;
+            if (epi == EPI_ADD) *o += acc[v];
+            else *o = acc[v];
+        }
+    }
+}
+
 void kq_groups(KqP &p, int nseg) {
     int acc = 0;
     for (int i = 0; i < 3; i++) {
@@ -248,16 +418,23 @@ void kq_launch(const KqP &p, hipStream_t st) {
     hipLaunchKernelGGL((gemm_q4k_kernel<GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
+void k6_launch(const KqP &p, hipStream_t st) {
+    const int slots = (p.n_rg + 7) / 8;
+    hipLaunchKernelGGL(gemm_q6k_kernel, dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+}
+
 }  // namespace
 
-bool gemm_kq_supported(int ty, size_t K) { return ty == T_Q4_K && K % 256 == 0 && K > 0; }
+bool gemm_kq_supported(int ty, size_t K) { return (ty == T_Q4_K || ty == T_Q6_K) && K % 256 == 0 && K > 0; }
 
 bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st) {
-    if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d || !act.bsums) return false;
+    if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d) return false;
+    const int ty = segs[0].w.ty;
+    if (ty == T_Q4_K && !act.bsums) return false;
     KqP p{};
     for (int i = 0; i < nseg; i++) {
         const GemvSeg &s = segs[i];
-        if (!gemm_kq_supported(s.w.ty, K) || s.w.cols != (size_t)K || !s.w.data || !s.out) return false;
+        if (s.w.ty != ty || !gemm_kq_supported(s.w.ty, K) || s.w.cols != (size_t)K || !s.w.data || !s.out) return false;
         p.w[i] = s.w.data;
         p.rb[i] = s.w.rb();
         p.rows[i] = (int)s.w.rows;
@@ -272,13 +449,14 @@ bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, 
     p.d = act.d;
     p.bsums = act.bsums;
     kq_groups(p, nseg);
-    kq_launch<false>(p, st);
+    if (ty == T_Q6_K) k6_launch(p, st);
+    else kq_launch<false>(p, st);
     return true;
 }
 
 bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
                         hipStream_t st) {
-    if (n_tok < 1 || !act.qs || !act.d || !act.bsums || gate.ty != up.ty || !gemm_kq_supported(gate.ty, K) ||
+    if (n_tok < 1 || !act.qs || !act.d || !act.bsums || gate.ty != up.ty || gate.ty != T_Q4_K || !gemm_kq_supported(gate.ty, K) ||
         gate.cols != (size_t)K || up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
         return false;
     KqP p{};

@@ -134,7 +134,8 @@ def test_rmsnorm_then_quant_bitwise(oracle, cuda, k):
 
 def _gemv(ty, w, rows, k, act, act_f32, n_tok, cuda, gemm=False):
     L = R.lib()
-    wd = dev(w, cuda)
+    # the weight buffer keeps the library's 4096 readable bytes past the last row
+    wd = dev(np.concatenate([w, np.zeros(4096, np.uint8)]), cuda)
     out = torch.zeros(n_tok * rows, dtype=torch.float32, device=cuda)
     qs, d, s, isum, bs = act if act is not None else (None,) * 5
     p = lambda t: t.data_ptr() if t is not None else None
@@ -168,16 +169,17 @@ def test_gemv_matches_oracle_rows(oracle, cuda, ty):
                 assert np.all(np.abs(got[t] - want) <= 1e-5 * mag + 1e-6), (ty, k, n_tok)
 
 
-@pytest.mark.parametrize("ty", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0, Q4_K, Q6_K])
 def test_gemm_matches_oracle_rows(oracle, cuda, ty):
     """The int8-MFMA prompt GEMM against the oracle's block dots, for row and
     token counts that are not multiples of the 32×32 tiles (Q4_K: Q8_K
-    activations, superblock sums with the 6-bit scales and mins)."""
+    activations, superblock sums with the 6-bit scales and mins; Q6_K: signed
+    16-value sub-block scales on K=16 MFMAs)."""
     import ggml_np as G
     r = oracle.Rng(31 + ty)
     shapes = ((128, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130))
-    if ty == Q4_K:
-        shapes = ((256, 40, 9), (512, 200, 33), (4096, 96, 70), (1024, 300, 130))
+    if ty in (Q4_K, Q6_K):
+        shapes = ((256, 40, 9), (512, 200, 33), (4096, 96, 70), (1024, 300, 130), (8192, 64, 512))
     for k, rows, n_tok in shapes:
         w = r.random_weight(ty, rows, k)
         x = (np.random.default_rng(k + n_tok).uniform(-1, 1, (n_tok, k)) * 2).astype(np.float32)
@@ -297,7 +299,7 @@ def test_model_logits_match_oracle(oracle, cuda, arch, ty, kv, tol):
 
 
 @pytest.mark.parametrize("arch,ty", [("llama", Q4_0), ("llama", Q8_0), ("qwen3", Q4_0), ("gemma2", Q8_0), ("llama", Q4_K),
-                                     ("qwen3", Q4_K)])
+                                     ("qwen3", Q4_K), ("llama", Q6_K), ("qwen3", Q6_K)])
 def test_prompt_batches_through_gemm_match_oracle(oracle, cuda, arch, ty):
     """Prompt batches of 24 and 40 tokens run the int8-MFMA GEMM (fused Q/K/V,
     wo, gate/up with SwiGLU/GELU, down) and must match the oracle like decode."""
