@@ -235,6 +235,14 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         d_moe_yg_ = dalloc<float>(allocs_, mb * E);
         d_moe_rows_ = dalloc<int>(allocs_, mb * nu);
         d_moe_rw_ = dalloc<float>(allocs_, mb * nu);
+        // device-side grouping of prompt batches (grouped expert GEMMs)
+        moe_max_tiles_ = moe_group_max_tiles((int)mb, (int)nu, (int)c.n_expert);
+        d_moe_off_ = dalloc<int>(allocs_, c.n_expert + 1);
+        d_moe_rtok_ = dalloc<int>(allocs_, mb * nu);
+        d_moe_rslot_ = dalloc<int>(allocs_, mb * nu);
+        d_moe_tile_e_ = dalloc<int>(allocs_, moe_max_tiles_);
+        d_moe_tile_r0_ = dalloc<int>(allocs_, moe_max_tiles_);
+        d_moe_ntiles_ = dalloc<int>(allocs_, 1);
     }
     cap_.resize(8);
     RIE_HIP_CHECK(hipDeviceSynchronize());
@@ -642,6 +650,47 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
             return true;
         }
         launch_moe_combine(d_moe_y_, d_moe_w_, 1, k, E, d_o_, EPI_STORE, st_);
+    } else if (moe_grouped_ok(L)) {
+        // Prompt batch, on the device: the routed pairs grouped by expert, one grouped
+        // GEMM launch for every expert's gate/up (activation rows gathered through the
+        // token map, hidden rows in gathered order), the hidden's quantization, one for
+        // every expert's down projection (rows scattered to their pair slots), and the
+        // per-token combine in ascending expert order (cpu.rs:487-513).
+        launch_moe_group(d_moe_sel_, n, k, ne, d_moe_off_, d_moe_rtok_, d_moe_rslot_, d_moe_tile_e_, d_moe_tile_r0_, d_moe_ntiles_, st_);
+        check_launch("moe group");
+        GroupTiles g;
+        g.tile_e = d_moe_tile_e_;
+        g.tile_r0 = d_moe_tile_r0_;
+        g.n_tiles = d_moe_ntiles_;
+        g.off = d_moe_off_;
+        g.amap = d_moe_rtok_;
+        g.max_tiles = moe_max_tiles_;
+        DevWeight ge = L.gate, ue = L.up, de = L.down;  // expert 0's matrices; the others follow at wstride
+        ge.rows = ue.rows = (size_t)ff;
+        de.rows = (size_t)E;
+        g.wstride = (size_t)ff * L.gate.rb();
+        const ActQ8 &ax = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
+        if (!launch_gemm_glu(ge, ue, ax, n * k, E, d_h_, ff, c.gelu, nullptr, st_, &g)) throw rt_err("grouped expert gate/up launch rejected");
+        check_launch("moe gate/up");
+        mark("moe_gate_up_glu");
+        const int dfmt = act_format(L.down.ty);
+        const ActQ8 &ah = dfmt == ACT_Q8K ? actk_ : act0_;
+        launch_quant_only(d_h_, ff, n * k, ff, dfmt, ah, st_);
+        GroupTiles g2 = g;
+        g2.amap = nullptr;
+        g2.omap = d_moe_rslot_;
+        g2.wstride = (size_t)E * L.down.rb();
+        GemvSeg sd{de, d_moe_y_, E, EPI_STORE};
+        if (!launch_gemm(&sd, 1, ah, n * k, ff, st_, &g2)) throw rt_err("grouped expert down launch rejected");
+        check_launch("moe down");
+        mark("moe_down");
+        if (direct && !shared && !capture_) {
+            launch_moe_combine(d_moe_y_, d_moe_w_, n, k, E, d_x_, EPI_ADD, st_);
+            check_launch("moe");
+            mark("moe_combine");
+            return true;
+        }
+        launch_moe_combine(d_moe_y_, d_moe_w_, n, k, E, d_o_, EPI_STORE, st_);
     } else {
         std::vector<int> sel((size_t)n * k);
         std::vector<float> w((size_t)n * k);
@@ -687,6 +736,15 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
     check_launch("moe");
     mark("moe_combine");
     return false;
+}
+
+// The device-grouped prompt path needs the int8 MFMA GEMMs for the experts' matrices:
+// a gated pair (Q4_0, Q8_0 or Q4_K) and a down projection with a GEMM.
+bool HipBackend::moe_grouped_ok(const DevLayer &L) const {
+    const size_t E = m_.cfg.n_embd, ff = L.ff;
+    const int gt = L.gate.ty;
+    return L.gate.ty == L.up.ty && (gt == T_Q4_0 || gt == T_Q8_0 || gt == T_Q4_K) && gemm_supported(gt, E) &&
+           gemm_supported(L.down.ty, ff) && d_moe_off_ != nullptr;
 }
 
 void HipBackend::forward(const uint32_t *tokens, size_t n, size_t pos, bool all_logits, float *logits, size_t logits_len) {

@@ -135,6 +135,10 @@ class HipBackend {
     float *d_router_ = nullptr, *d_moe_w_ = nullptr, *d_moe_y_ = nullptr;
     float *d_moe_xn_ = nullptr, *d_moe_xg_ = nullptr, *d_moe_yg_ = nullptr, *d_moe_rw_ = nullptr;
     int *d_moe_sel_ = nullptr, *d_moe_rows_ = nullptr;
+    int *d_moe_off_ = nullptr, *d_moe_rtok_ = nullptr, *d_moe_rslot_ = nullptr, *d_moe_tile_e_ = nullptr, *d_moe_tile_r0_ = nullptr,
+        *d_moe_ntiles_ = nullptr;
+    int moe_max_tiles_ = 0;
+    bool moe_grouped_ok(const DevLayer &L) const;
     float *d_kcap_ = nullptr;  // K after norm/RoPE when capturing
     int n_amax_part_ = 64;
 

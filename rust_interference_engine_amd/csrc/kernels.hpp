@@ -134,16 +134,37 @@ bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff,
                              const float *act_f32, int K, float *h, int gelu, const ActQ8 *hq, hipStream_t st,
                              const NormIn *nin = nullptr);
 
+// ---- grouped expert GEMMs (prompt batches of MoE layers, moe_ffn cpu.rs:487-524) ----
+// The routed (token, slot) pairs of a batch, grouped by expert on the device: gathered
+// row r of expert e lies in [off[e], off[e+1]); token tiles of GROUP_BN rows list their
+// expert and first row.  A grouped GEMM runs one weight matrix per expert (expert e's at
+// w + e·wstride) over that expert's rows only; its activation row for gathered row r is
+// amap[r] (or r), its output row omap[r] (or r).
+constexpr int GROUP_BN = 64;
+struct GroupTiles {
+    const int *tile_e = nullptr, *tile_r0 = nullptr, *n_tiles = nullptr, *off = nullptr;
+    const int *amap = nullptr, *omap = nullptr;
+    size_t wstride = 0;
+    int max_tiles = 0;  // grid bound: token tiles of the largest possible grouping
+};
+// sel [n_tok·k] (ascending experts per token) → off [n_exp+1], row_tok / row_slot
+// [n_tok·k] (token t and pair index t·k + j of each gathered row), the tile table
+// (tile_e / tile_r0 [max_tiles], *n_tiles).  One workgroup; n_exp ≤ 512.
+void launch_moe_group(const int *sel, int n_tok, int k, int n_exp, int *off, int *row_tok, int *row_slot, int *tile_e, int *tile_r0,
+                      int *n_tiles, hipStream_t st);
+int moe_group_max_tiles(int n_tok, int k, int n_exp);
+
 // ---- gemm_kq.hip (prefill, Q4_K × Q8_K on int8 MFMA; reached through gemm.hip) ----
 bool gemm_kq_supported(int ty, size_t K);
-bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st);
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr);
 bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                        hipStream_t st);
+                        hipStream_t st, const GroupTiles *grp = nullptr);
 
 // ---- gemm.hip (prefill, int8 MFMA) ----
 bool gemm_supported(int ty, size_t K);
-bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st);
+// grp: one segment per expert group (the segment's rows are one expert's; see GroupTiles)
+bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr);
 bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                     float *scratch, hipStream_t st);
+                     float *scratch, hipStream_t st, const GroupTiles *grp = nullptr);
 
 }  // namespace rie

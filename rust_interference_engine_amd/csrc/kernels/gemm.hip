@@ -44,7 +44,30 @@ struct GemmP {
     const int8_t *qs;
     const float *d;
     int n_tok, K;
+    int grouped;    // expert groups: one matrix per expert (grp), 64-token tiles from its table
+    GroupTiles grp;
 };
+
+// A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
+// [r0, r_end) of expert e (false: a tile past the grouping's count)
+struct GTileRows {
+    int r0, r_end, e;
+};
+__device__ __forceinline__ bool gtile_rows(const GemmP &p, int tg, int bn, GTileRows &t) {
+    if (!p.grouped) {
+        t.r0 = tg * bn;
+        t.r_end = p.n_tok;
+        t.e = 0;
+        return true;
+    }
+    if (tg >= *p.grp.n_tiles) return false;
+    t.e = p.grp.tile_e[tg];
+    t.r0 = p.grp.tile_r0[tg];
+    t.r_end = min(p.grp.off[t.e + 1], t.r0 + bn);
+    return true;
+}
+__device__ __forceinline__ int gact_row(const GemmP &p, int r) { return p.grouped && p.grp.amap ? p.grp.amap[r] : r; }
+__device__ __forceinline__ int gout_row(const GemmP &p, int r) { return p.grouped && p.grp.omap ? p.grp.omap[r] : r; }
 
 // weight unit: blocks b and b+1 of one row (36 or 68 bytes from a dword boundary)
 template <int TY>
@@ -93,27 +116,26 @@ struct StageRegs {
     WUnit<TY> w;
 };
 
+// tokA: the activation row of the thread's token (tid / (256/BN)); tokD: of token tid
+// (tid < BN); woff: the expert's byte offset in a grouped launch
 template <int TY, bool GLU, int BN>
-__device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int t0, int b0, int tid, StageRegs<TY, GLU, BN> &R) {
+__device__ __forceinline__ void stage_load(const GemmP &p, int sg, int row0, int tokA, int tokD, size_t woff, int b0, int tid,
+                                           StageRegs<TY, GLU, BN> &R) {
     const int K = p.K, nb = K >> 5;
     {   // activation codes: thread → (token, part of its 128-byte chunk)
         constexpr int TPT = 256 / BN, NV = 128 / TPT / 16;  // threads per token, 16-byte loads per thread
-        const int tok = min(t0 + tid / TPT, p.n_tok - 1);
-        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 32 * b0 + 16 * NV * (tid % TPT));
+        const v4i *src = (const v4i *)(p.qs + (size_t)tokA * K + 32 * b0 + 16 * NV * (tid % TPT));
 #pragma unroll
         for (int i = 0; i < NV; i++) R.a[i] = src[i];
     }
-    if (tid < BN) {
-        const int tok = min(t0 + tid, p.n_tok - 1);
-        R.da = *(const float4 *)(p.d + (size_t)tok * nb + b0);
-    }
+    if (tid < BN) R.da = *(const float4 *)(p.d + (size_t)tokD * nb + b0);
     {   // weights: thread → (matrix, row, 2-block unit)
         const int nw = GLU ? (tid >> 7) : 0;
         const int idx = tid & 127;
         const int row = min(row0 + (idx >> 1), p.rows[GLU ? 0 : sg] - 1);
         if (GLU || tid < 128) {
             const int s = GLU ? nw : sg;
-            load_wunit<TY>(p.w[s] + (size_t)row * p.rb[s], b0 + 2 * (idx & 1), R.w);
+            load_wunit<TY>(p.w[s] + woff + (size_t)row * p.rb[s], b0 + 2 * (idx & 1), R.w);
         }
     }
 }
@@ -172,7 +194,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * G_BM;
-    const int t0 = tg * BN;
+    GTileRows tr;
+    if (!gtile_rows(p, tg, BN, tr)) return;  // whole workgroup: uniform
+    const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
+    const int tokA = gact_row(p, min(tr.r0 + tid / (256 / BN), tr.r_end - 1));
+    const int tokD = gact_row(p, min(tr.r0 + tid % BN, tr.r_end - 1));
     const int h = l >> 5, m = l & 31;
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int wrow = wr * 32 + m;  // this lane's weight row in the tile (B operand / result column)
@@ -192,7 +218,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
 
     const int n_stages = p.K / (32 * G_KC);
     StageRegs<TY, GLU, BN> R;
-    stage_load<TY, GLU, BN>(p, sg, row0, t0, 0, tid, R);
+    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, tid, R);
     stage_store<TY, GLU, BN>(st[0], tid, R);
     __syncthreads();
     // Per stage: all operands of the stage's KC blocks from LDS, then the
@@ -201,7 +227,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     constexpr int P = G_KC * NT * NW;
     for (int s = 0; s < n_stages; s++) {
         const bool more = s + 1 < n_stages;
-        if (more) stage_load<TY, GLU, BN>(p, sg, row0, t0, (s + 1) * G_KC, tid, R);
+        if (more) stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, (s + 1) * G_KC, tid, R);
         const GemmStage<TY, GLU, BN> &S = st[s & 1];
         v4i bw[G_KC][NW], av[G_KC][NT];
         float bs[G_KC][NW], as[G_KC][NT];
@@ -265,11 +291,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int tok = t0 + wc * 32 * NT + 32 * t + 16 * h + v;
-            if (tok < p.n_tok) {
+            const int r = tr.r0 + wc * 32 * NT + 32 * t + 16 * h + v;
+            if (r < tr.r_end) {
                 float y = acc[0][t][v];
                 if constexpr (GLU) y = (p.glu == 2 ? gelu_tanh_f(acc[0][t][v]) : silu_f(acc[0][t][v])) * acc[NW - 1][t][v];
-                float *o = out + (size_t)tok * ld + row;
+                float *o = out + (size_t)gout_row(p, r) * ld + row;
                 if (epi == EPI_ADD) *o += y;
                 else *o = y;
             }
@@ -283,11 +309,18 @@ bool gemm_supported(int ty, size_t K) {
 // 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
 // then 64-token tiles (one 32-token tile per wave)
 template <int TY, bool GLU>
-static void launch_t(GemmP p, hipStream_t st) {
+static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp) {
     const int slots = (p.n_rg + 7) / 8;
     int nt = 2;
     if (slots * 8 * ((p.n_tok + 127) / 128) < 512 && p.n_tok > 64) nt = 1;
     p.n_tg = (p.n_tok + 64 * nt - 1) / (64 * nt);
+    if (grp) {  // 64-token tiles from the grouping's table
+        static_assert(GROUP_BN == 64, "grouped tiles are one 32-token tile per wave");
+        nt = 1;
+        p.grouped = 1;
+        p.grp = *grp;
+        p.n_tg = grp->max_tiles;
+    }
     if (nt == 2) hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
     else hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
@@ -303,10 +336,10 @@ static void set_groups(GemmP &p, int nseg) {
     p.n_rg = acc;
 }
 
-bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st) {
-    if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act)) return false;
+bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp) {
+    if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act) || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
-    if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st);
+    if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st, grp);
     GemmP p{};
     for (int i = 0; i < nseg; i++) {
         const GemvSeg &s = segs[i];
@@ -325,15 +358,16 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (ty == T_Q4_0) launch_t<T_Q4_0, false>(p, st);
-    else launch_t<T_Q8_0, false>(p, st);
+    if (ty == T_Q4_0) launch_t<T_Q4_0, false>(p, st, grp);
+    else launch_t<T_Q8_0, false>(p, st, grp);
     return true;
 }
 
 bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                     float *scratch, hipStream_t st) {
+                     float *scratch, hipStream_t st, const GroupTiles *grp) {
     (void)scratch;
-    if (gemm_kq_supported(gate.ty, K)) return launch_gemm_kq_glu(gate, up, act, n_tok, K, h, ld, gelu, st);
+    if (grp && grp->max_tiles < 1) return false;
+    if (gemm_kq_supported(gate.ty, K)) return launch_gemm_kq_glu(gate, up, act, n_tok, K, h, ld, gelu, st, grp);
     if (n_tok < 1 || !operands_ok(act) || gate.ty != up.ty || !gemm_supported(gate.ty, K) || gate.cols != (size_t)K ||
         up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
         return false;
@@ -353,8 +387,8 @@ bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, true>(p, st);
-    else launch_t<T_Q8_0, true>(p, st);
+    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, true>(p, st, grp);
+    else launch_t<T_Q8_0, true>(p, st, grp);
     return true;
 }
 

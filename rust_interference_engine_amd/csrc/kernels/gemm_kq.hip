@@ -54,9 +54,33 @@ struct KqP {
     const float *d;
     const int16_t *bsums;
     int n_tok, K;
+    int grouped;     // expert groups: one matrix per expert (grp), token tiles from its table
+    GroupTiles grp;
 };
 
 constexpr int KQ_BM = 64, KQ_BN = 64;
+static_assert(KQ_BN == GROUP_BN, "grouped tiles are built for this token tile");
+
+// A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
+// [r0, r_end) of expert e (false: a tile past the grouping's count, nothing to do).
+struct TileRows {
+    int r0, r_end, e;
+};
+__device__ __forceinline__ bool tile_rows(const KqP &p, int tg, TileRows &t) {
+    if (!p.grouped) {
+        t.r0 = tg * KQ_BN;
+        t.r_end = p.n_tok;
+        t.e = 0;
+        return true;
+    }
+    if (tg >= *p.grp.n_tiles) return false;
+    t.e = p.grp.tile_e[tg];
+    t.r0 = p.grp.tile_r0[tg];
+    t.r_end = min(p.grp.off[t.e + 1], t.r0 + KQ_BN);
+    return true;
+}
+__device__ __forceinline__ int act_row(const KqP &p, int r) { return p.grouped && p.grp.amap ? p.grp.amap[r] : r; }
+__device__ __forceinline__ int out_row(const KqP &p, int r) { return p.grouped && p.grp.omap ? p.grp.omap[r] : r; }
 constexpr int KA_ST = 128 + 16;  // activation bytes per token in LDS (one half superblock, padded)
 constexpr int KW_ST = 64 + 16;   // weight nibble bytes per row in LDS (one half superblock, padded)
 
@@ -81,19 +105,20 @@ struct KqRegs {
 };
 
 // stage loads for half hs of superblock sb
+// tokA: the activation row of the thread's token (tid/4); tokD: of token tid (tid < 64);
+// woff: the expert's byte offset in a grouped launch
 template <bool GLU>
-__device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int t0, int sb, int hs, int tid, KqRegs &R) {
+__device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int tokA, int tokD, size_t woff, int sb, int hs, int tid,
+                                        KqRegs &R) {
     const int K = p.K, nsb = K >> 8;
     {
-        const int tok = min(t0 + (tid >> 2), p.n_tok - 1);
-        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 256 * sb + 128 * hs + 32 * (tid & 3));
+        const v4i *src = (const v4i *)(p.qs + (size_t)tokA * K + 256 * sb + 128 * hs + 32 * (tid & 3));
         R.a[0] = src[0];
         R.a[1] = src[1];
     }
     if (tid < KQ_BN) {
-        const int tok = min(t0 + tid, p.n_tok - 1);
-        R.da = p.d[(size_t)tok * nsb + sb];
-        const v4i *bsrc = (const v4i *)(p.bsums + (size_t)tok * (K >> 4) + 16 * sb);
+        R.da = p.d[(size_t)tokD * nsb + sb];
+        const v4i *bsrc = (const v4i *)(p.bsums + (size_t)tokD * (K >> 4) + 16 * sb);
         R.bs[0] = bsrc[0];
         R.bs[1] = bsrc[1];
     }
@@ -101,7 +126,7 @@ __device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int t0, 
         const int nw = GLU ? (tid >> 7) : 0, idx = tid & 127, u = idx & 1;
         const int s = GLU ? nw : sg;
         const int row = min(row0 + (idx >> 1), p.rows[GLU ? 0 : sg] - 1);
-        const uint8_t *blk = p.w[s] + (size_t)row * p.rb[s] + 144 * (size_t)sb;
+        const uint8_t *blk = p.w[s] + woff + (size_t)row * p.rb[s] + 144 * (size_t)sb;
         const v4i *q = (const v4i *)(blk + 16 + 64 * hs + 32 * u);
         R.wq[0] = wload(q);
         R.wq[1] = wload(q + 1);
@@ -164,7 +189,11 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
-    const int t0 = tg * KQ_BN;
+    TileRows tr;
+    if (!tile_rows(p, tg, tr)) return;  // whole workgroup: uniform
+    const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
+    const int tokA = act_row(p, min(tr.r0 + (tid >> 2), tr.r_end - 1));
+    const int tokD = act_row(p, min(tr.r0 + (tid & 63), tr.r_end - 1));
     const int h = l >> 5, m = l & 31;
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int wrow = wr * 32 + m;   // this lane's weight row (B operand / result column)
@@ -183,12 +212,12 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
         }
     const int n_stages = (p.K >> 8) * 2;
     KqRegs R;
-    kq_load<GLU>(p, sg, row0, t0, 0, 0, tid, R);
+    kq_load<GLU>(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
     kq_store<GLU>(st[0], tid, R);
     __syncthreads();
     for (int s = 0; s < n_stages; s++) {
         const int hs = s & 1;
-        if (s + 1 < n_stages) kq_load<GLU>(p, sg, row0, t0, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        if (s + 1 < n_stages) kq_load<GLU>(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
         const KqStage<GLU> &S = st[s & 1];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -233,11 +262,11 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     const int epi = p.epi[sg];
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-        const int tok = t0 + wc * 32 + 16 * h + v;
-        if (tok < p.n_tok) {
+        const int r = tr.r0 + wc * 32 + 16 * h + v;
+        if (r < tr.r_end) {
             float y = acc[0][v];
             if constexpr (GLU) y = (p.glu == 2 ? gelu_tanh_f(acc[0][v]) : silu_f(acc[0][v])) * acc[NW - 1][v];
-            float *o = out + (size_t)tok * ld + row;
+            float *o = out + (size_t)out_row(p, r) * ld + row;
             if (epi == EPI_ADD) *o += y;
             else *o = y;
         }
@@ -274,17 +303,17 @@ __device__ __forceinline__ void ld3_a2(const uint8_t *p, uint32_t (&w)[3], uint3
 }
 
 // thread → (row tid/4, part tid%4): values l + 32i of the half, l in 8·part..+8, i = 0..3
-__device__ __forceinline__ void k6_load(const KqP &p, int sg, int row0, int t0, int sb, int hs, int tid, K6Regs &R) {
+__device__ __forceinline__ void k6_load(const KqP &p, int sg, int row0, int tokA, int tokD, size_t woff, int sb, int hs, int tid,
+                                        K6Regs &R) {
     const int K = p.K, nsb = K >> 8;
     {
-        const int tok = min(t0 + (tid >> 2), p.n_tok - 1);
-        const v4i *src = (const v4i *)(p.qs + (size_t)tok * K + 256 * sb + 128 * hs + 32 * (tid & 3));
+        const v4i *src = (const v4i *)(p.qs + (size_t)tokA * K + 256 * sb + 128 * hs + 32 * (tid & 3));
         R.a[0] = src[0];
         R.a[1] = src[1];
     }
-    if (tid < KQ_BN) R.da = p.d[(size_t)min(t0 + tid, p.n_tok - 1) * nsb + sb];
+    if (tid < KQ_BN) R.da = p.d[(size_t)tokD * nsb + sb];
     const int row = min(row0 + (tid >> 2), p.rows[sg] - 1), part = tid & 3;
-    const uint8_t *blk = p.w[sg] + (size_t)row * p.rb[sg] + 210 * (size_t)sb;
+    const uint8_t *blk = p.w[sg] + woff + (size_t)row * p.rb[sg] + 210 * (size_t)sb;
     ld3_a2(blk + 64 * hs + 8 * part, R.lo, R.sh_l);
     ld3_a2(blk + 64 * hs + 32 + 8 * part, R.hi, R.sh_h);
     ld3_a2(blk + 128 + 32 * hs + 8 * part, R.qh, R.sh_q);
@@ -342,7 +371,11 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
-    const int t0 = tg * KQ_BN;
+    TileRows tr;
+    if (!tile_rows(p, tg, tr)) return;  // whole workgroup: uniform
+    const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
+    const int tokA = act_row(p, min(tr.r0 + (tid >> 2), tr.r_end - 1));
+    const int tokD = act_row(p, min(tr.r0 + (tid & 63), tr.r_end - 1));
     const int h = l >> 5, m = l & 31;
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int wrow = wr * 32 + m;
@@ -358,12 +391,12 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     }
     const int n_stages = (p.K >> 8) * 2;
     K6Regs R;
-    k6_load(p, sg, row0, t0, 0, 0, tid, R);
+    k6_load(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
     k6_store(st[0], tid, R);
     __syncthreads();
     for (int s = 0; s < n_stages; s++) {
         const int hs = s & 1;
-        if (s + 1 < n_stages) k6_load(p, sg, row0, t0, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        if (s + 1 < n_stages) k6_load(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
         const K6Stage &S = st[s & 1];
 #pragma unroll
         for (int k = 0; k < 8; k++) {  // 16-value sub-blocks of the half
@@ -393,16 +426,16 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     const int epi = p.epi[sg];
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-        const int tok = t0 + wc * 32 + 16 * h + v;
-        if (tok < p.n_tok) {
-            float *o = out + (size_t)tok * ld + row;
+        const int r = tr.r0 + wc * 32 + 16 * h + v;
+        if (r < tr.r_end) {
+            float *o = out + (size_t)out_row(p, r) * ld + row;
             if (epi == EPI_ADD) *o += acc[v];
             else *o = acc[v];
         }
     }
 }
 
-void kq_groups(KqP &p, int nseg) {
+void kq_groups(KqP &p, int nseg, const GroupTiles *grp) {
     int acc = 0;
     for (int i = 0; i < 3; i++) {
         if (i < nseg) acc += (p.rows[i] + KQ_BM - 1) / KQ_BM;
@@ -410,6 +443,11 @@ void kq_groups(KqP &p, int nseg) {
     }
     p.n_rg = acc;
     p.n_tg = (p.n_tok + KQ_BN - 1) / KQ_BN;
+    if (grp) {
+        p.grouped = 1;
+        p.grp = *grp;
+        p.n_tg = grp->max_tiles;
+    }
 }
 
 template <bool GLU>
@@ -427,8 +465,8 @@ void k6_launch(const KqP &p, hipStream_t st) {
 
 bool gemm_kq_supported(int ty, size_t K) { return (ty == T_Q4_K || ty == T_Q6_K) && K % 256 == 0 && K > 0; }
 
-bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st) {
-    if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d) return false;
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp) {
+    if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
     if (ty == T_Q4_K && !act.bsums) return false;
     KqP p{};
@@ -448,14 +486,15 @@ bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, 
     p.qs = act.qs;
     p.d = act.d;
     p.bsums = act.bsums;
-    kq_groups(p, nseg);
+    kq_groups(p, nseg, grp);
     if (ty == T_Q6_K) k6_launch(p, st);
     else kq_launch<false>(p, st);
     return true;
 }
 
 bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
-                        hipStream_t st) {
+                        hipStream_t st, const GroupTiles *grp) {
+    if (grp && grp->max_tiles < 1) return false;
     if (n_tok < 1 || !act.qs || !act.d || !act.bsums || gate.ty != up.ty || gate.ty != T_Q4_K || !gemm_kq_supported(gate.ty, K) ||
         gate.cols != (size_t)K || up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
         return false;
@@ -475,7 +514,7 @@ bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 
     p.qs = act.qs;
     p.d = act.d;
     p.bsums = act.bsums;
-    kq_groups(p, 1);
+    kq_groups(p, 1, grp);
     kq_launch<true>(p, st);
     return true;
 }

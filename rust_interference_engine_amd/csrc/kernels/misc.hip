@@ -3,6 +3,7 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -284,6 +285,67 @@ __global__ __launch_bounds__(256) void moe_shared_add_kernel(const float *__rest
 
 void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *x, int n_tok, int E, float *out, hipStream_t st) {
     hipLaunchKernelGGL(moe_shared_add_kernel, dim3(n_tok), dim3(256), 0, st, ys, gate_inp, x, E, out);
+}
+
+// Grouping of a prompt batch's routed pairs by expert (the assign lists of
+// moe_ffn, cpu.rs:489-501), on the device: counts, their exclusive prefix, each
+// pair's gathered row, and the token tiles of every expert.  Within an expert the
+// rows follow the arrival order of an LDS counter: any order gives the same
+// results, since a row's values depend on its own token only, and the combine sums
+// each token's experts in ascending order from the pair index.  Expert ids outside
+// [0, n_exp) (only from non-finite router logits) are dropped.
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int *__restrict__ sel, int n_pairs, int k, int n_exp, int *off,
+                                                         int *row_tok, int *row_slot, int *tile_e, int *tile_r0, int *n_tiles) {
+    __shared__ int cnt[512], fill[512], base[513], tbase[513];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < n_exp; e += 1024) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int a = tid; a < n_pairs; a += 1024) {
+        const int e = sel[a];
+        if ((unsigned)e < (unsigned)n_exp) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0, tacc = 0;
+        for (int e = 0; e < n_exp; e++) {
+            base[e] = acc;
+            tbase[e] = tacc;
+            acc += cnt[e];
+            tacc += (cnt[e] + GROUP_BN - 1) / GROUP_BN;
+        }
+        base[n_exp] = acc;
+        tbase[n_exp] = tacc;
+        *n_tiles = tacc;
+    }
+    __syncthreads();
+    for (int e = tid; e <= n_exp; e += 1024) off[e] = base[e];
+    for (int a = tid; a < n_pairs; a += 1024) {
+        const int e = sel[a];
+        if ((unsigned)e >= (unsigned)n_exp) continue;
+        const int r = base[e] + atomicAdd(&fill[e], 1);
+        row_tok[r] = a / k;
+        row_slot[r] = a;
+    }
+    for (int e = tid; e < n_exp; e += 1024)
+        for (int i = 0; i < tbase[e + 1] - tbase[e]; i++) {
+            tile_e[tbase[e] + i] = e;
+            tile_r0[tbase[e] + i] = base[e] + i * GROUP_BN;
+        }
+}
+
+int moe_group_max_tiles(int n_tok, int k, int n_exp) {
+    // the full tiles of all pairs, plus at most one partial tile per expert that has rows
+    const int pairs = n_tok * k;
+    return (pairs + GROUP_BN - 1) / GROUP_BN + std::min(n_exp, pairs);
+}
+
+void launch_moe_group(const int *sel, int n_tok, int k, int n_exp, int *off, int *row_tok, int *row_slot, int *tile_e, int *tile_r0,
+                      int *n_tiles, hipStream_t st) {
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, st, sel, n_tok * k, k, n_exp, off, row_tok, row_slot, tile_e, tile_r0,
+                       n_tiles);
 }
 
 void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
