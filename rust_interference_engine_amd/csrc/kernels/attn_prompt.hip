@@ -10,6 +10,15 @@
 // probability p, so every score and every output is an f32-accurate sum of
 // exact products; only the summation order differs from the CPU path.
 //
+// Turbo4 caches (KVT = 2, head dim 128, one rotation block per row): attention
+// runs in the rotated domain as the reference's does (cpu.rs:584-632, turbo.rs:
+// 178-250).  The query is rotated and quantized to Q8_0 first (turbo_query_kernel,
+// bitwise the reference's codes), and its dequantized values d·q8 take the place of
+// q.  Key and value tiles are the int8 Lloyd–Max levels of their codes (exact in
+// f16); a key row's scale/46 multiplies its scores, a value row's scale/46 its
+// probabilities before the P·V product (axpy_rotated_4's factor), and the output
+// goes back through the inverse rotation (FWHT, 1/√128, signs) in the epilogue.
+//
 // Work split: a workgroup (4 waves) owns one KV head and a block of query rows;
 // each wave owns 32 tokens of one query head.  Scores are computed transposed,
 // Sᵀ = K·Qᵀ (v_mfma_f32_32x32x16_f16: lane l holds token l mod 32 and 16 cache
@@ -22,6 +31,8 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <type_traits>
+
 namespace rie {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -32,37 +43,71 @@ namespace {
 constexpr int PT = 32;         // cache positions per tile
 constexpr int VROW = PT * 2 + 8;   // bytes per transposed V row in LDS (padded: 8-row steps shift by 16 banks)
 
+// Lloyd–Max levels of the Turbo4 codes as int8 (turbo.rs:126-127), four per
+// dword for v_perm lookups
+constexpr int8_t TQ_LEVELS[16] = {-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126};
+constexpr uint32_t tq_word(int i) {
+    return (uint32_t)(uint8_t)TQ_LEVELS[4 * i] | ((uint32_t)(uint8_t)TQ_LEVELS[4 * i + 1] << 8) |
+           ((uint32_t)(uint8_t)TQ_LEVELS[4 * i + 2] << 16) | ((uint32_t)(uint8_t)TQ_LEVELS[4 * i + 3] << 24);
+}
+// four codes (one per byte, 0..15) → their int8 levels (one per byte)
+__device__ __forceinline__ uint32_t tq_levels4(uint32_t codes) {
+    const uint32_t s7 = codes & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(tq_word(1), tq_word(0), s7), hi = __builtin_amdgcn_perm(tq_word(3), tq_word(2), s7);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((codes >> 3) & 0x01010101u) | 0x0C0C0C0Cu);  // 0xFF where code ≥ 8
+    return (hi & m) | (lo & ~m);
+}
+// byte e of a dword of int8 levels as the bits of an f16 (exact: |level| ≤ 126)
+__device__ __forceinline__ uint32_t tq_f16(uint32_t lv, int e) {
+    const _Float16 h = (_Float16)(float)(int)(int8_t)((lv >> (8 * e)) & 0xff);
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+// x = hi + lo with hi = x rounded to 11 significant bits in f32 (exact in f16, so
+// its conversion cannot round) and lo = x − hi exactly, then rounded to f16
+// (|lo| ≤ 2^-11·|x|).  Rounding x to f16 and computing lo from that value instead
+// is not safe: the compiler may convert x twice with different instructions
+// (v_cvt_f16_f32 for lo, v_cvt_pk_f16_f32 for the packed hi), and values just
+// above a rounding midpoint have come out of the two on opposite sides, an error
+// of one f16 ulp of x.
 __device__ __forceinline__ half8 split_hi(const float (&x)[8], half8 &lo) {
-    half8 hi;
+    f32x8 hi, r;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        hi[i] = (_Float16)x[i];
-        lo[i] = (_Float16)(x[i] - (float)hi[i]);
+        hi[i] = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x[i]) + 0x1000u) & 0xFFFFE000u);
+        r[i] = x[i] - hi[i];
     }
-    return hi;
+    lo = __builtin_convertvector(r, half8);
+    return __builtin_convertvector(hi, half8);
 }
 
 __device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
-// LDS bytes of one wave group's K and transposed V tile
-template <int HD>
-constexpr int tile_bytes() { return PT * (HD * 2 + 16) + HD * VROW; }
+// LDS bytes of one wave group's K and transposed V tile (+ the rows' score and
+// probability factors of a Turbo4 tile)
+template <int HD, int KVT = 0>
+constexpr int tile_bytes() { return PT * (HD * 2 + 16) + HD * VROW + (KVT == 2 ? 2 * PT * 4 : 0); }
 // merge scratch of NW groups: running maxima and sums, then one 32-dim output tile per group
 template <int NW>
 constexpr int merge_bytes() { return NW > 1 ? 2 * NW * 256 * 4 + (NW - 1) * 256 * 16 * 4 : 0; }
-template <int HD, int NW>
-constexpr int prompt_lds_bytes() { return 2 * NW * tile_bytes<HD>() > merge_bytes<NW>() ? 2 * NW * tile_bytes<HD>() : merge_bytes<NW>(); }
+template <int HD, int NW, int KVT = 0>
+constexpr int prompt_lds_bytes() {
+    return 2 * NW * tile_bytes<HD, KVT>() > merge_bytes<NW>() ? 2 * NW * tile_bytes<HD, KVT>() : merge_bytes<NW>();
+}
 
 // NW groups of 4 waves: group q handles the tiles q, q + NW, …, and the groups'
 // online-softmax states are merged through LDS at the end.
-template <int HD, int NW>
+template <int HD, int NW, int KVT>
 __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
+    static_assert(KVT == 0 || (KVT == 2 && HD == 128), "Turbo4 tiles: one 128-dim rotation block per row");
     constexpr int KS = HD / 16;          // 16-dim k-steps of the score product
     constexpr int DT = HD / 32;          // 32-dim output tiles
     constexpr int KROW = HD * 2 + 16;    // bytes per K row in LDS (padded)
     constexpr int NCH = (PT * HD / 8 + 255) / 256;  // 16-byte chunks per thread per tile (K and V each)
+    constexpr int RB = KVT == 2 ? HD / 2 : HD * 2;   // cache row bytes
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int TB = tile_bytes<HD>();
+    constexpr int TB = tile_bytes<HD, KVT>();
     const int grp = threadIdx.x >> 8;
     uint8_t *const tiles = lds + grp * 2 * TB;  // this group's two tile buffers: K rows, then Vᵀ rows
 
@@ -115,12 +160,17 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
         }
     }
 
-    const uint8_t *kc = a.k_cache + (size_t)g * a.slots * (HD * 2);
-    const uint8_t *vc = a.v_cache + (size_t)g * a.slots * (HD * 2);
-    // one tile in flight in registers: K as 16-byte row chunks, V as two positions × 8 dims
+    const uint8_t *kc = a.k_cache + (size_t)g * a.slots * RB;
+    const uint8_t *vc = a.v_cache + (size_t)g * a.slots * RB;
+    const uint16_t *ksc = KVT == 2 ? a.k_scale + (size_t)g * a.slots : nullptr;
+    const uint16_t *vsc = KVT == 2 ? a.v_scale + (size_t)g * a.slots : nullptr;
+    // one tile in flight in registers: f16 K as 16-byte row chunks and V as two
+    // positions × 8 dims; Turbo4 K as 8 code bytes of a row, V as 4 code bytes of two
+    // rows, and the row scale of position tid (K) or tid − 32 (V)
     struct Regs {
         u32x4 k[NCH];
         u32x4 v[2];
+        uint32_t sc;
     };
     // Every lane issues the same loads (indices past the tile's data repeat valid
     // ones, and ring slots wrap without a branch: slots ≥ 32 = the tile length).
@@ -128,21 +178,66 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
         const int P0 = k0 + tile * PT;
         const int slot0 = P0 % a.slots;
         const int span = p_hi - P0;  // positions past p_hi repeat row p_hi
-        auto row = [&](int off) {
+        auto slot = [&](int off) {
             const int s0 = slot0 + min(off, span);
-            return (size_t)(s0 >= a.slots ? s0 - a.slots : s0) * (HD * 2);
+            return (size_t)(s0 >= a.slots ? s0 - a.slots : s0);
         };
+        auto row = [&](int off) { return slot(off) * RB; };
+        if constexpr (KVT == 2) {
+            const uint2 kk = *(const uint2 *)(kc + row(tid >> 3) + 8 * (tid & 7));  // position tid/8, bytes 8·(tid%8)..+8
+            r.k[0] = u32x4{kk.x, kk.y, 0u, 0u};
 #pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            const int ch = min(tid + 256 * c, PT * HD / 8 - 1);
-            r.k[c] = *(const u32x4 *)(kc + row(ch / (HD / 8)) + (ch % (HD / 8)) * 16);
+            for (int rr = 0; rr < 2; rr++)  // positions 2·(tid/16) + rr, bytes 4·(tid%16)..+4
+                r.v[rr][0] = *(const uint32_t *)(vc + row(2 * (tid >> 4) + rr) + 4 * (tid & 15));
+            r.sc = tid < 32 ? ksc[slot(tid)] : vsc[slot(min(tid - 32, PT - 1))];
+        } else {
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const int ch = min(tid + 256 * c, PT * HD / 8 - 1);
+                r.k[c] = *(const u32x4 *)(kc + row(ch / (HD / 8)) + (ch % (HD / 8)) * 16);
+            }
+            const int vi = min(tid, 2 * HD - 1);  // positions 2·(vi % 16) + {0, 1}, dims 8·(vi / 16) .. +8
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++) r.v[rr] = *(const u32x4 *)(vc + row(2 * (vi & 15) + rr) + (vi >> 4) * 16);
         }
-        const int vi = min(tid, 2 * HD - 1);  // positions 2·(vi % 16) + {0, 1}, dims 8·(vi / 16) .. +8
-#pragma unroll
-        for (int rr = 0; rr < 2; rr++) r.v[rr] = *(const u32x4 *)(vc + row(2 * (vi & 15) + rr) + (vi >> 4) * 16);
     };
     auto stage = [&](const Regs &r, int buf) {
         uint8_t *kb = tiles + buf * TB, *vb = kb + PT * KROW;
+        if constexpr (KVT == 2) {
+            // K row tid/8: code bytes 8c..8c+8 (c = tid%8) of chunk c/2 hold dims
+            // 32(c/2) + 8(c%2) + 0..7 (low nibbles) and the same + 16 (high nibbles)
+            const int pos = tid >> 3, c = tid & 7;
+            const uint32_t w[2] = {r.k[0][0], r.k[0][1]};
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                uint32_t lv[2];
+#pragma unroll
+                for (int q = 0; q < 2; q++) lv[q] = tq_levels4((half ? (w[q] >> 4) : w[q]) & 0x0F0F0F0Fu);
+                u32x4 hv;
+#pragma unroll
+                for (int q = 0; q < 4; q++) hv[q] = tq_f16(lv[q >> 1], 2 * (q & 1)) | (tq_f16(lv[q >> 1], 2 * (q & 1) + 1) << 16);
+                *(u32x4 *)(kb + pos * KROW + (32 * (c >> 1) + 8 * (c & 1) + 16 * half) * 2) = hv;
+            }
+            // Vᵀ: code bytes 4j..4j+4 (j = tid%16) of positions 2·(tid/16) + {0, 1}: dims
+            // 32(j/4) + 4(j%4) + 0..3 and the same + 16, one dword = the two positions
+            const int pp = tid >> 4, j = tid & 15;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const uint32_t l0 = tq_levels4((half ? (r.v[0][0] >> 4) : r.v[0][0]) & 0x0F0F0F0Fu);
+                const uint32_t l1 = tq_levels4((half ? (r.v[1][0] >> 4) : r.v[1][0]) & 0x0F0F0F0Fu);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int dim = 32 * (j >> 2) + 4 * (j & 3) + 16 * half + e;
+                    *(uint32_t *)(vb + dim * VROW + 4 * pp) = tq_f16(l0, e) | (tq_f16(l1, e) << 16);
+                }
+            }
+            // per-position factors: score × scale_k/46 (in log2 units), probability ×
+            // scale_v/46 × 2^8 (undone in the epilogue; it keeps the f16 halves of small
+            // weighted probabilities out of the subnormal range)
+            float *fac = (float *)(vb + HD * VROW);
+            if (tid < 2 * PT) fac[tid] = h2f(r.sc) * (tid < PT ? LOG2E_F / 46.0f : 256.0f / 46.0f);
+            return;
+        }
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
             const int ch = tid + 256 * c;
@@ -186,6 +281,7 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
         fetch(min(tile + 3 * NW, last), x);
         k_s = tiles + (it & 1) * TB;
         v_s = k_s + PT * KROW;
+        const float *fk = (const float *)(v_s + HD * VROW), *fv = fk + PT;  // Turbo4 row factors
         const int P0 = k0 + tile * PT;
         const bool work = tile < n_tiles && wave_on && P0 <= w_pmax && P0 + PT - 1 >= w_smin;
         if (work) {
@@ -197,8 +293,13 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
                 s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], s, 0, 0, 0);
                 s2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], s2, 0, 0, 0);
             }
+            if constexpr (KVT == 2) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) s[v] = (s[v] + s2[v]) * LOG2E_F;
+                for (int v = 0; v < 16; v++) s[v] = (s[v] + s2[v]) * fk[8 * (v >> 2) + 4 * h + (v & 3)];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; v++) s[v] = (s[v] + s2[v]) * LOG2E_F;
+            }
             // lane: token col, positions P0 + 8(v/4) + 4h + v%4; scores in log2 units (q carries log2 e)
             if (a.softcap > 0.0f) {
                 const float cl = a.softcap * LOG2E_F;  // the cap in the same units
@@ -219,7 +320,9 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
             // The reference maximum m moves only when a score exceeds it by more than
             // 2^8, so probabilities stay ≤ 256 and the accumulators are rescaled rarely
             // (exact either way: m cancels in O / l).
-            const bool grow = mx > m + 8.0f;
+            // (Turbo4: 2^2, so a weighted probability ≤ 4·scale_v·2^8/46 stays an f16 for row
+            // scales — the rotated row's RMS — up to 2944)
+            const bool grow = mx > m + (KVT == 2 ? 2.0f : 8.0f);
             if (__builtin_amdgcn_ballot_w64(grow)) {
                 const float m_new = grow ? mx : m;
                 const float alpha = grow ? exp2_hw(m - m_new) : 1.0f;  // m = −inf: 0
@@ -236,6 +339,10 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
             for (int v = 0; v < 16; v++) {
                 pv[v] = exp2_hw(s[v] - mref);
                 l_half += pv[v];
+            }
+            if constexpr (KVT == 2) {  // the value rows' scale/46 (l keeps the plain probabilities)
+#pragma unroll
+                for (int v = 0; v < 16; v++) pv[v] *= fv[8 * (v >> 2) + 4 * h + (v & 3)];
             }
             half8 ph[2], pl[2];
 #pragma unroll
@@ -312,11 +419,67 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
     const float l_tot = l_half + xor_f<32>(l_half);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     // lane: token col, dims 32d + 8(v/4) + 4h + v%4
+    if constexpr (KVT == 2) {
+        // Rᵀ o (turbo.rs:113-117): the normalized FWHT of the rotated output (stages of
+        // distance 1, 2, …, 64 as fwht runs them: x[j] = a + b, x[j+h] = a − b), then the
+        // signs.  Distance 4 is the half-wave (lane ± 32), the others are in the lane.
+        float x[DT][16];
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) x[d][v] = o[d][v] * (inv * (1.0f / 256.0f));
+        auto bfly = [](float &lo, float &hi) {
+            const float p = lo, q = hi;
+            lo = p + q;
+            hi = p - q;
+        };
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) bfly(x[d][v], x[d][v + 1]);
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (!(v & 2)) bfly(x[d][v], x[d][v + 2]);
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const float other = xor_f<32>(x[d][v]);
+                x[d][v] = h == 0 ? x[d][v] + other : other - x[d][v];
+            }
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (!(v & 4)) bfly(x[d][v], x[d][v + 4]);
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (!(v & 8)) bfly(x[d][v], x[d][v + 8]);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            bfly(x[0][v], x[1][v]);
+            bfly(x[2 % DT][v], x[3 % DT][v]);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            bfly(x[0][v], x[2 % DT][v]);
+            bfly(x[1 % DT][v], x[3 % DT][v]);
+        }
+        const float nrm = 1.0f / sqrtf((float)HD);
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) o[d][v] = x[d][v] * nrm * a.turbo_signs[32 * d + 8 * (v >> 2) + 4 * h + (v & 3)];
+    }
 #pragma unroll
     for (int d = 0; d < DT; d++) {
         float y[16];
 #pragma unroll
-        for (int v = 0; v < 16; v++) y[v] = o[d][v] * inv;
+        for (int v = 0; v < 16; v++) y[v] = KVT == 2 ? o[d][v] : o[d][v] * inv;
         if (tok_ok) {
             float *dst = a.att + (size_t)t * qd + (size_t)head * hd + 32 * d + 4 * h;
 #pragma unroll
@@ -366,20 +529,63 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
     }
 }
 
-template <int HD, int NW>
+template <int HD, int NW, int KVT>
 void launch_nw(const AttnArgs &a, dim3 grid, hipStream_t st) {
-    constexpr int lds = prompt_lds_bytes<HD, NW>();
-    static const bool attr = hipFuncSetAttribute((const void *)attn_prompt_f16_kernel<HD, NW>,
+    constexpr int lds = prompt_lds_bytes<HD, NW, KVT>();
+    static const bool attr = hipFuncSetAttribute((const void *)attn_prompt_f16_kernel<HD, NW, KVT>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess;
     (void)attr;
-    hipLaunchKernelGGL((attn_prompt_f16_kernel<HD, NW>), grid, dim3(256 * NW), lds, st, a);
+    hipLaunchKernelGGL((attn_prompt_f16_kernel<HD, NW, KVT>), grid, dim3(256 * NW), lds, st, a);
+}
+
+// Turbo4 query of one (token, head) per wave (turbo.rs:103-112, then the x86
+// Q8_0 quantizer, kernels/avx2.rs:153-184, as cpu.rs:584-600 prepares it): lane l
+// holds dims 2l, 2l+1; signs, the FWHT stages of distance 1 (in the lane) and
+// 2..64 (lane exchanges), ×1/√128, then Q8_0 per 32 dims (16 lanes); writes d·q8.
+__global__ __launch_bounds__(64) void turbo_query_kernel(const float *__restrict__ q, int qd, const float *__restrict__ signs,
+                                                        float *__restrict__ qhat) {
+    const int t = blockIdx.y, hq = blockIdx.x, lane = threadIdx.x;
+    const size_t base = (size_t)t * qd + (size_t)hq * 128;
+    float x0 = q[base + 2 * lane] * signs[2 * lane], x1 = q[base + 2 * lane + 1] * signs[2 * lane + 1];
+    {
+        const float a = x0, b = x1;
+        x0 = a + b;
+        x1 = a - b;
+    }
+    auto stage = [&](auto oc) {
+        constexpr int o = decltype(oc)::value;  // lane distance; dim distance 2·o
+        const float p0 = xor_f<o>(x0), p1 = xor_f<o>(x1);
+        const bool lo = (lane & o) == 0;
+        x0 = lo ? x0 + p0 : p0 - x0;
+        x1 = lo ? x1 + p1 : p1 - x1;
+    };
+    stage(std::integral_constant<int, 1>{});
+    stage(std::integral_constant<int, 2>{});
+    stage(std::integral_constant<int, 4>{});
+    stage(std::integral_constant<int, 8>{});
+    stage(std::integral_constant<int, 16>{});
+    stage(std::integral_constant<int, 32>{});
+    const float s = 1.0f / sqrtf(128.0f);
+    x0 *= s;
+    x1 *= s;
+    float amax = fmaxf(fabsf(x0), fabsf(x1));
+    amax = fmaxf(amax, xor_f<1>(amax));
+    amax = fmaxf(amax, xor_f<2>(amax));
+    amax = fmaxf(amax, xor_f<4>(amax));
+    amax = fmaxf(amax, xor_f<8>(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int c0 = max(-127, min(127, (int)rintf(x0 * id))), c1 = max(-127, min(127, (int)rintf(x1 * id)));
+    qhat[base + 2 * lane] = d * (float)c0;
+    qhat[base + 2 * lane + 1] = d * (float)c1;
 }
 
 }  // namespace
 
 bool attention_prompt_mfma_ok(const AttnArgs &a) {
     const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
-    return a.kv_type == 0 && a.n_tok > 1 && !a.d_pos0 && a.slots >= 32 && (a.hd == 32 || a.hd == 64 || a.hd == 96 || a.hd == 128) && G >= 1 &&
+    const bool cache_ok = a.kv_type == 0 || (a.kv_type == 2 && a.hd == 128 && a.turbo_signs && a.k_scale && a.v_scale && a.part);
+    return cache_ok && a.n_tok > 1 && !a.d_pos0 && a.slots >= 32 && (a.hd == 32 || a.hd == 64 || a.hd == 96 || a.hd == 128) && G >= 1 &&
            G <= 8 && a.n_head == G * a.n_kv && (a.att_fmt != ACT_Q8_0 || (a.att_q.qs && a.att_q.d));
 }
 
@@ -388,11 +594,19 @@ bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st) {
     const int G = a.n_head / a.n_kv;
     const int wpt = G < 4 ? G : 4, tbw = 4 / wpt, hgroups = (G + 3) / 4;
     const dim3 grid((a.n_tok + 32 * tbw - 1) / (32 * tbw), a.n_kv * hgroups);
+    if (a.kv_type == 2) {
+        // the rotated, quantized queries go to the range-partial buffer (unused on this path)
+        hipLaunchKernelGGL(turbo_query_kernel, dim3(a.n_head, a.n_tok), dim3(64), 0, st, a.q, a.n_head * 128, a.turbo_signs, a.part);
+        AttnArgs b = a;
+        b.q = a.part;
+        launch_nw<128, 2, 2>(b, grid, st);
+        return true;
+    }
     switch (a.hd) {
-    case 32: launch_nw<32, 2>(a, grid, st); break;
-    case 64: launch_nw<64, 2>(a, grid, st); break;
-    case 96: launch_nw<96, 2>(a, grid, st); break;
-    default: launch_nw<128, 2>(a, grid, st); break;
+    case 32: launch_nw<32, 2, 0>(a, grid, st); break;
+    case 64: launch_nw<64, 2, 0>(a, grid, st); break;
+    case 96: launch_nw<96, 2, 0>(a, grid, st); break;
+    default: launch_nw<128, 2, 0>(a, grid, st); break;
     }
     return true;
 }

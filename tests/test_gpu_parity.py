@@ -461,6 +461,74 @@ def test_prompt_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv
                         f"hd {hd} G {G} layer {layer} token {p} head {hq}: {err}"
 
 
+def _turbo_attention_f64(oracle, q, krows, kscales, vrows, vscales, hd):
+    """cpu.rs:584-632 over a Turbo4 cache in float64: the query rotated and
+    quantized to Q8_0 (the oracle's), integer level dots per 32-value chunk
+    (dot_rotated_4, turbo.rs:178-193), softmax, the weighted levels
+    (axpy_rotated_4) and the inverse rotation (turbo.rs:113-117)."""
+    lv = np.array([-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126], np.float64)
+    n = krows.shape[0]
+
+    def codes(rows):
+        c = np.empty((n, hd), np.int64)
+        for ch in range(hd // 32):
+            c[:, 32 * ch:32 * ch + 16] = rows[:, 16 * ch:16 * ch + 16] & 0xF
+            c[:, 32 * ch + 16:32 * ch + 32] = rows[:, 16 * ch:16 * ch + 16] >> 4
+        return c
+    qa = oracle.quantize_q8_0(oracle.turbo_rotate(q.astype(np.float32)))
+    qs, dq = qa["qs"].reshape(-1).astype(np.float64), qa["d"].astype(np.float64)
+    ks = kscales.view(np.float16).astype(np.float64)
+    vs = vscales.view(np.float16).astype(np.float64)
+    s = ((lv[codes(krows)] * qs).reshape(n, hd // 32, 32).sum(axis=2) * dq).sum(axis=1) * ks / 46.0
+    w = np.exp(s - s.max())
+    vv = vs[:, None] * lv[codes(vrows)] / 46.0
+    orot = ((w / w.sum())[:, None] * vv).sum(axis=0)
+    return oracle.turbo_rotate(orot.astype(np.float32), inverse=True).astype(np.float64), s, vv
+
+
+@pytest.mark.parametrize("nh,nkv", [(8, 2), (6, 2), (12, 2), (8, 8), (16, 2)])
+def test_turbo_prompt_attention_matches_f64_on_captured_rows(oracle, cuda, nh, nkv):
+    """Prompt attention over a Turbo4 cache (head dim 128: rotated, Q8_0-quantized
+    queries against the level tiles on f16 matrix cores, inverse rotation in the
+    epilogue) against float64 on the GPU's own captured queries and cache rows,
+    for prompt batches starting at positions 0, 64 and 128 (causal tile edges,
+    1 to 8 query heads per KV head)."""
+    hd = 128
+
+    def mut(s):
+        s.head_dim, s.n_head, s.n_head_kv, s.rope_dim = hd, nh, nkv, hd
+    n_ctx = 160
+    spec, g, _ = _pair(oracle, "llama", Q8_0, 2, n_ctx=n_ctx, max_batch=64, mutate=mut)
+    g.set_capture(True)
+    G, qd = nh // nkv, nh * hd
+    toks = [(i * 53 + 11) % spec.n_vocab for i in range(150)]
+    for pos0, end in ((0, 64), (64, 128), (128, 150)):
+        n = end - pos0
+        g.forward(toks[pos0:end], pos0)
+        for layer in range(spec.n_layer):
+            q = g.capture(layer, 3, n * qd).reshape(n, nh, hd)
+            att = g.capture(layer, 2, n * qd).reshape(n, nh, hd)
+            kr, ksc = g.kv_layer(layer, 0, nkv, n_ctx)
+            vr, vsc = g.kv_layer(layer, 1, nkv, n_ctx)
+            # largest decoded V value up to each position, in the rotated and the original
+            # domain: a relative error δ_j of probability j moves the output by δ_j·p_j·R⁻¹vv_j
+            vrun = []
+            for kv in range(nkv):
+                _, _, vv = _turbo_attention_f64(oracle, q[0, 0], kr[kv, :end], ksc[kv, :end], vr[kv, :end], vsc[kv, :end], hd)
+                m = [max(np.abs(r).max(), np.abs(oracle.turbo_rotate(r.astype(np.float32), inverse=True)).max()) for r in vv]
+                vrun.append(np.maximum.accumulate(m))
+            for t in range(n):
+                p = pos0 + t
+                for hq in range(nh):
+                    kv = hq // G
+                    ref, sc, _ = _turbo_attention_f64(oracle, q[t, hq], kr[kv, :p + 1], ksc[kv, :p + 1], vr[kv, :p + 1],
+                                                      vsc[kv, :p + 1], hd)
+                    vmax = vrun[kv][p]
+                    err = np.max(np.abs(att[t, hq] - ref))
+                    assert err <= (8 * 2.0 ** -24 * np.max(np.abs(sc)) + 5e-6) * vmax + 2e-6 * vmax + 1e-6, \
+                        f"G {G} layer {layer} token {p} head {hq}: {err}"
+
+
 @pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
 def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv):
     """Single-token attention (the fused launch: prep, append, context ranges,
