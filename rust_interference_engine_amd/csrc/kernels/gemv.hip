@@ -158,8 +158,12 @@ constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 
 // NT threads (256 or 512): one pass of NT/LPR row groups × R rows covers a
 // 32-row tile in a single pass (all of a workgroup's loads issued up front).
-template <int TY, int LPR, int UPL, bool GLU, int R, int NT>
-__global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
+// PRO8 (Q4_0/Q8_0 weights with a norm input): the activation is made in the
+// prologue; a separate instance, so that every load before the prologue is
+// unconditional and the compiler's wait for x does not cover the weight stream.
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false>
+__global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p) {  // 512 threads: two workgroups per CU
+    static_assert(!PRO8 || TY == T_Q4_0 || TY == T_Q8_0, "the Q8_0 prologue serves Q4_0/Q8_0 weights");
     constexpr int GROUPS = NT / LPR;
     constexpr int STRIDE = LPR + DEC_PAD;
     constexpr int NW = GLU ? 2 : 1;
@@ -208,10 +212,28 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
         }
     };
     const int base0 = grp * R;
-    if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
+    // PRO8: x and the norm weight are requested before the weight stream, and the
+    // prologue's barriers order LDS only, so the activation is made while the
+    // weights are in flight (loads complete in issue order, and a full
+    // __syncthreads() would wait for the whole stream).
+    float4 xv[4], gv[4];  // values 16τ..16τ+15 of x and of the norm weight
+    if constexpr (PRO8) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[i] = gv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tid < (p.K >> 4)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xv[i] = ((const float4 *)(p.nin.x + 16 * tid))[i];
+                gv[i] = ((const float4 *)(p.nin.w + 16 * tid))[i];
+            }
+        }
+        load_pass(base0);  // unconditional (rows are clamped): a group without rows here drops its loads
+    } else {
+        if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
+    }
     bool have_act = false;
-    if constexpr (TY == T_Q4_0 || TY == T_Q8_0) {
-        if (p.nin.x) {
+    if constexpr (PRO8) {
+        {
             // The activation is Q8_0(RMSNorm(x)·w), made here once per workgroup:
             // thread τ normalizes values 16τ..16τ+15 (a 32-block is a thread pair)
             // into LDS, then every lane reads its slice (quantizer: quant.hip).
@@ -220,15 +242,10 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             __shared__ int s_i[128];
             const int K = p.K, nthr = K >> 4;
             const bool act = tid < nthr;
-            float4 xv[4], gv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = gv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float ss = 0.0f;
             if (act) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    xv[i] = ((const float4 *)(p.nin.x + 16 * tid))[i];
-                    gv[i] = ((const float4 *)(p.nin.w + 16 * tid))[i];
                     ss = fmaf(xv[i].x, xv[i].x, ss);
                     ss = fmaf(xv[i].y, xv[i].y, ss);
                     ss = fmaf(xv[i].z, xv[i].z, ss);
@@ -237,7 +254,7 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
             }
             ss = wave_sum(ss, 64);
             if ((tid & 63) == 0) s_red[tid >> 6] = ss;
-            __syncthreads();
+            lds_barrier();
             const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
             float y[16];
             float amax = 0.0f;
@@ -275,7 +292,7 @@ __global__ __launch_bounds__(NT) void gemv_dec_kernel(DecP p) {
                     s_i[tid >> 1] = isum;
                 }
             }
-            __syncthreads();
+            lds_barrier();
 #pragma unroll
             for (int k = 0; k < UPL; k++) {
                 const uint4 *src = (const uint4 *)(s_q + 64 * uu[k]);
@@ -533,12 +550,23 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         if (i < nseg) blocks += (p.seg[i].rows + p.tr - 1) / p.tr;
         p.blk_end[i] = blocks;
     }
-#define RIE_DEC(L, UP)                                                                                            \
-    do {                                                                                                          \
-        if (p.glu && nt == 512) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 512>), dim3(blocks), dim3(512), lds, st, p);    \
-        else if (p.glu && nt == 1024) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 1024>), dim3(blocks), dim3(1024), lds, st, p); \
-        else if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256>), dim3(blocks), dim3(256), lds, st, p);      \
-        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256>), dim3(blocks), dim3(256), lds, st, p);                \
+    constexpr bool Q8PRO = TY == T_Q4_0 || TY == T_Q8_0;
+    const bool pro = Q8PRO && p.nin.x;
+#define RIE_DEC_P(L, UP, PR)                                                                                          \
+    do {                                                                                                              \
+        if (p.glu && nt == 512) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 512, PR>), dim3(blocks), dim3(512), lds, st, p);    \
+        else if (p.glu && nt == 1024) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 1024, PR>), dim3(blocks), dim3(1024), lds, st, p); \
+        else if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);      \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);                \
+    } while (0)
+#define RIE_DEC(L, UP)                           \
+    do {                                         \
+        if constexpr (Q8PRO) {                   \
+            if (pro) RIE_DEC_P(L, UP, true);     \
+            else RIE_DEC_P(L, UP, false);        \
+        } else {                                 \
+            RIE_DEC_P(L, UP, false);             \
+        }                                        \
     } while (0)
     if (upl == 1) {
         switch (lpr) {
@@ -552,6 +580,7 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         RIE_DEC(256, 2);
     }
 #undef RIE_DEC
+#undef RIE_DEC_P
     return true;
 }
 
