@@ -250,10 +250,11 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
 
 HipBackend::~HipBackend() {
     if (st_) (void)hipStreamSynchronize(st_);
-    for (auto &kv : graphs_) {
-        (void)hipGraphExecDestroy(kv.second.exec);
-        (void)hipGraphDestroy(kv.second.graph);
-    }
+    for (auto *m : {&graphs_, &greedy_graphs_})
+        for (auto &kv : *m) {
+            (void)hipGraphExecDestroy(kv.second.exec);
+            (void)hipGraphDestroy(kv.second.graph);
+        }
     for (void *p : allocs_) (void)hipFree(p);
     if (d_blob_) (void)hipFree(d_blob_);
     if (st_) (void)hipStreamDestroy(st_);
@@ -538,18 +539,25 @@ void HipBackend::head(int first, int m) {
     const ModelConfig &c = m_.cfg;
     const int E = (int)c.n_embd;
     const DevWeight *ws[1] = {&out_w_};
-    // the normalized rows are kept in d_xn_ for Backend::hidden
     const int fmt = act_format(out_w_.ty);
     const float *xr = d_x_ + (size_t)first * E;
-    if (fmt == ACT_F32) {
-        launch_rmsnorm(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, E, 0, st_);
-    } else {
-        launch_rmsnorm_quant(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+    GemvSeg s{out_w_, d_logits_, (int)c.n_vocab, EPI_STORE};
+    head_first_ = first;
+    // one row, Q8_0/Q8_K head: the head GEMV normalizes and quantizes the row
+    // itself; Backend::hidden then forms the normalized row on demand
+    const NormIn nin{xr, out_norm_, c.rms_eps};
+    head_normed_ = !(m == 1 && !capture_ && fmt != ACT_F32 && gemv_norm_ok(out_w_.ty, E) &&
+                     launch_gemv(&s, 1, fmt == ACT_Q8K ? actk_ : act0_, d_xn_, 1, E, st_, &nin));
+    if (head_normed_) {  // the normalized rows are kept in d_xn_ for Backend::hidden
+        if (fmt == ACT_F32) {
+            launch_rmsnorm(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, E, 0, st_);
+        } else {
+            launch_rmsnorm_quant(xr, E, out_norm_, c.rms_eps, m, E, d_xn_, fmt, fmt == ACT_Q8K ? actk_ : act0_, st_);
+        }
+        mark("rmsnorm_quant");
+        matmul(&s, 1, m, E);
     }
     (void)ws;
-    mark("rmsnorm_quant");
-    GemvSeg s{out_w_, d_logits_, (int)c.n_vocab, EPI_STORE};
-    matmul(&s, 1, m, E);
     mark("matmul_output");
     const size_t total = (size_t)m * c.n_vocab;
     if (c.logit_scale != 1.0f) launch_scale(d_logits_, total, c.logit_scale, st_);
@@ -799,6 +807,34 @@ void HipBackend::decode_step_graph(size_t pos) {
     RIE_HIP_CHECK(hipGraphLaunch(it->second.exec, st_));
 }
 
+// One greedy step as a graph (per attention range count): run_layers at the
+// device-resident position d_pos_[0], then the advancing argmax.
+void HipBackend::greedy_step_graph(size_t pos) {
+    const int ns = splits_for(1, pos);
+    auto it = greedy_graphs_.find(ns);
+    if (it == greedy_graphs_.end()) {
+        DecodeGraph dg;
+        in_capture_ = true;
+        RIE_HIP_CHECK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+        try {
+            run_layers(1, 0, d_pos_, false, ns);
+            launch_argmax_step(d_logits_, (int)m_.cfg.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, d_gen_, d_pos_,
+                               (int)std::max<size_t>(n_ctx_, 1), st_);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(st_, &g);
+            if (g) (void)hipGraphDestroy(g);
+            in_capture_ = false;
+            throw;
+        }
+        RIE_HIP_CHECK(hipStreamEndCapture(st_, &dg.graph));
+        in_capture_ = false;
+        RIE_HIP_CHECK(hipGraphInstantiate(&dg.exec, dg.graph, nullptr, nullptr, 0));
+        it = greedy_graphs_.emplace(ns, dg).first;
+    }
+    RIE_HIP_CHECK(hipGraphLaunch(it->second.exec, st_));
+}
+
 int HipBackend::splits_for(size_t n, size_t pos) const {
     return attention_splits((int)n, (int)m_.cfg.n_head_kv, (int)(pos + n));
 }
@@ -806,6 +842,15 @@ int HipBackend::splits_for(size_t n, size_t pos) const {
 const float *HipBackend::hidden(size_t *rows) {
     *rows = hidden_rows_;
     if (!hidden_rows_) return nullptr;
+    if (!head_normed_) {  // the head normalized its row in its prologue: form it here (the same kernel as the head's rows)
+        const ModelConfig &c = m_.cfg;
+        const int E = (int)c.n_embd, fmt = act_format(out_w_.ty);
+        RIE_HIP_CHECK(hipSetDevice(device_));
+        launch_rmsnorm_quant(d_x_ + (size_t)head_first_ * E, E, out_norm_, c.rms_eps, (int)hidden_rows_, E, d_xn_, fmt,
+                             fmt == ACT_Q8K ? actk_ : act0_, st_);
+        check_launch("hidden rows");
+        head_normed_ = true;
+    }
     hidden_host_.resize(hidden_rows_ * m_.cfg.n_embd);
     RIE_HIP_CHECK(hipMemcpyAsync(hidden_host_.data(), d_xn_, hidden_host_.size() * 4, hipMemcpyDeviceToHost, st_));
     RIE_HIP_CHECK(hipStreamSynchronize(st_));
@@ -843,6 +888,19 @@ void HipBackend::generate_greedy(size_t pos, size_t n_gen, uint32_t *out) {
     if (n_gen == 0) return;
     const ModelConfig &c = m_.cfg;
     RIE_HIP_CHECK(hipSetDevice(device_));
+    if (use_graph_ && !capture_) {
+        // every step one graph launch: the layers, the head and the argmax, which
+        // records the token, feeds it to the next step and advances the position
+        RIE_HIP_CHECK(hipMemcpyAsync(d_gen_, d_tokens_, 4, hipMemcpyDeviceToDevice, st_));
+        launch_set_int(d_pos_, (int)pos, st_);
+        launch_set_int(d_pos_ + 1, 0, st_);
+        check_launch("greedy setup");
+        for (size_t i = 0; i < n_gen; i++) greedy_step_graph(pos + i);
+        RIE_HIP_CHECK(hipMemcpyAsync(out, d_gen_, n_gen * 4, hipMemcpyDeviceToHost, st_));
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        hidden_rows_ = 1;
+        return;
+    }
     for (size_t i = 0; i < n_gen; i++) {
         RIE_HIP_CHECK(hipMemcpyAsync(d_gen_ + i, d_tokens_, 4, hipMemcpyDeviceToDevice, st_));
         if (use_graph_ && !capture_) {

@@ -98,6 +98,7 @@ class HipBackend {
     void head(int first, int m);
     void check_launch(const char *what);
     void decode_step_graph(size_t pos);
+    void greedy_step_graph(size_t pos);
     // context ranges per (token, kv head) in attention; the same for every batch size so
     // a token's attention does not depend on how its batch was formed
     int splits_for(size_t n, size_t pos) const;  // attention context ranges of a launch
@@ -143,6 +144,8 @@ class HipBackend {
     int n_amax_part_ = 64;
 
     size_t hidden_rows_ = 0;
+    int head_first_ = 0;        // first batch row of the last head launch
+    bool head_normed_ = true;   // d_xn_ holds the head's normalized rows (else Backend::hidden forms them)
     std::vector<float> hidden_host_;
     bool capture_ = false;
     std::vector<std::vector<std::vector<float>>> cap_;  // [what][layer]
@@ -159,6 +162,7 @@ class HipBackend {
         hipGraphExec_t exec = nullptr;
     };
     std::map<int, DecodeGraph> graphs_;  // by attention range count
+    std::map<int, DecodeGraph> greedy_graphs_;  // the same with the advancing argmax (generate_greedy)
     bool in_capture_ = false;
 };
 

@@ -45,18 +45,37 @@ __global__ __launch_bounds__(256) void argmax_stage1(const float *__restrict__ x
     }
 }
 
-__global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float *pval, int n_part, uint32_t *out) {
+// gen != nullptr (greedy steps replayed in a graph): the token is also stored at
+// gen[step[1] + 1] (below gen_cap), and the position step[0] and index step[1]
+// advance by one for the next step.
+__global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float *pval, int n_part, uint32_t *out, uint32_t *gen, int *step,
+                                                    int gen_cap) {
     const int tid = threadIdx.x;
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = tid; i < n_part; i += 64) amax_merge(v, idx, pval[i], pidx[i]);
     xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
-    if (tid == 0) *out = idx == 0x7fffffff ? 0u : (uint32_t)idx;
+    if (tid == 0) {
+        const uint32_t t = idx == 0x7fffffff ? 0u : (uint32_t)idx;
+        *out = t;
+        if (gen) {
+            const int g = step[1] + 1;
+            if (g < gen_cap) gen[g] = t;
+            step[1] = g;
+            step[0] += 1;
+        }
+    }
 }
 
 void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st) {
     hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
-    hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx);
+    hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx, nullptr, nullptr, 0);
+}
+
+void launch_argmax_step(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, uint32_t *gen,
+                        int *step, int gen_cap, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
+    hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx, gen, step, gen_cap);
 }
 
 // ---- argmax without device allocation ----

@@ -22,7 +22,7 @@ namespace rie {
 constexpr int Q8_0_BLOCKS_PER_WG = 16;
 constexpr int Q8K_BLOCKS_PER_WG = 4;
 
-// ref_order: the norm's sum of squares in the reference's order (sumsq_ref_order).
+// ref_order: the norm's sum of squares in the reference's order (rms_scale_ref_wg).
 template <int FMT>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float *__restrict__ x, int ldx, const float *__restrict__ w,
                                                             float eps, int E, float *__restrict__ xn, ActQ8 act, int ref_order) {

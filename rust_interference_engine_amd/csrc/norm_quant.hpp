@@ -54,45 +54,52 @@ __device__ __forceinline__ float rms_scale_wg(const float *__restrict__ xr, int 
 // tree ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)) as exchanges at lane offsets 8, 4,
 // 2, 1 (each addition the reference's, operands commuted at most); then the
 // sequential tail s + x[i]·x[i] (not fused) over the last E % 16 values.  For
-// the same row this is the reference's sum bit for bit.  Lanes 16-63 repeat
-// lanes 0-15; every lane returns the sum.  Serial: E/16 dependent fmas.
-template <bool COH = false>
-__device__ __forceinline__ float sumsq_ref_order(const float *__restrict__ xr, int E) {
-    const int L = threadIdx.x & 15;
-    const int nj = E >> 4;
-    float acc = 0.0f;
-    int j = 0;
-    for (; j + 8 <= nj; j += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = ld_row<COH>(xr + 16 * (j + u) + L);
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc = fmaf(v[u], v[u], acc);
-    }
-    for (; j < nj; j++) {
-        const float v = ld_row<COH>(xr + 16 * j + L);
-        acc = fmaf(v, v, acc);
-    }
-    acc = acc + xor_f<8>(acc);
-    acc = acc + xor_f<4>(acc);
-    acc = acc + xor_f<2>(acc);
-    acc = acc + xor_f<1>(acc);
-    float s = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
-    for (int i = nj << 4; i < E; i++) {
-        const float v = ld_row<COH>(xr + i);
-        s = s + v * v;
-    }
-    return s;
-}
-
-// 1/√(Σx²/E + eps) with Σx² in the reference's order (sumsq_ref_order, by the
-// first wave), for a workgroup (red: 1 float of LDS).
+// the same row this is the reference's sum bit for bit.  Serial: E/16 dependent fmas.
+// 1/√(Σx²/E + eps) with Σx² in that order, for a workgroup of 256 threads (red:
+// 1 float of LDS; lanes 16-63 of the first wave repeat lanes 0-15).  The
+// row passes through LDS in chunks of 4096 values, one coalesced load round per
+// chunk, and the first wave runs the serial fma chains from LDS.
 template <bool COH = false>
 __device__ __forceinline__ float rms_scale_ref_wg(const float *__restrict__ xr, int E, float eps, float *red) {
-    __syncthreads();  // red may still be read by a previous call
-    if (threadIdx.x < 64) {
-        const float ss = sumsq_ref_order<COH>(xr, E);
-        if (threadIdx.x == 0) red[0] = 1.0f / sqrtf(ss / (float)E + eps);
+    constexpr int CH = 4096;
+    __shared__ float s_chunk[CH];
+    const int tid = threadIdx.x, L = tid & 15;
+    const int body = (E >> 4) << 4;  // values of the 16-lane chains; the rest is the tail
+    float acc = 0.0f;
+    __syncthreads();  // red and s_chunk may still be read by a previous call
+    for (int c0 = 0; c0 < body; c0 += CH) {
+        const int cn = min(CH, body - c0);
+#pragma unroll 4
+        for (int i = tid; i < cn; i += 256) s_chunk[i] = ld_row<COH>(xr + c0 + i);
+        __syncthreads();
+        if (tid < 64) {
+            const int nj = cn >> 4;
+            int j = 0;
+            for (; j + 8 <= nj; j += 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = s_chunk[16 * (j + u) + L];
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc = fmaf(v[u], v[u], acc);
+            }
+            for (; j < nj; j++) {
+                const float v = s_chunk[16 * j + L];
+                acc = fmaf(v, v, acc);
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < 64) {
+        acc = acc + xor_f<8>(acc);
+        acc = acc + xor_f<4>(acc);
+        acc = acc + xor_f<2>(acc);
+        acc = acc + xor_f<1>(acc);
+        float ss = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+        for (int i = body; i < E; i++) {
+            const float v = ld_row<COH>(xr + i);
+            ss = ss + v * v;
+        }
+        if (tid == 0) red[0] = 1.0f / sqrtf(ss / (float)E + eps);
     }
     __syncthreads();
     return red[0];
