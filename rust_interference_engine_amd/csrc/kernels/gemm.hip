@@ -9,7 +9,8 @@
 // so each block contributes (d_w·d_a)·isum exactly as the reference's block dot
 // does; only the order of the f32 sum over blocks differs.  Weights stay in
 // their ggml layout: a lane loads its row's 2-block unit (36 / 68 bytes, dword
-// aligned), unpacks the nibbles of its 16-value half and subtracts 8 bytewise.
+// aligned) per stage and writes its codes to LDS as int8, for Q4_0 with the
+// nibbles unpacked and 8 subtracted bytewise (once per workgroup, not per wave).
 //
 // Operand lane layout (checked by the parity tests): lane l supplies row
 // (l mod 32) and values 16·(l/32)..+16 of the block, for A (tokens) and B
@@ -49,22 +50,16 @@ struct GemmP {
 };
 
 // A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
-// [r0, r_end) of expert e (false: a tile past the grouping's count)
+// [r0, r_end) of expert e (e < 0: a tile past the grouping's count).  Returned by
+// value: the reference-parameter form kept the struct in scratch memory.
 struct GTileRows {
     int r0, r_end, e;
 };
-__device__ __forceinline__ bool gtile_rows(const GemmP &p, int tg, int bn, GTileRows &t) {
-    if (!p.grouped) {
-        t.r0 = tg * bn;
-        t.r_end = p.n_tok;
-        t.e = 0;
-        return true;
-    }
-    if (tg >= *p.grp.n_tiles) return false;
-    t.e = p.grp.tile_e[tg];
-    t.r0 = p.grp.tile_r0[tg];
-    t.r_end = min(p.grp.off[t.e + 1], t.r0 + bn);
-    return true;
+__device__ __forceinline__ GTileRows gtile_rows(const GemmP &p, int tg, int bn) {
+    if (!p.grouped) return GTileRows{tg * bn, p.n_tok, 0};
+    if (tg >= *p.grp.n_tiles) return GTileRows{0, 0, -1};
+    const int e = p.grp.tile_e[tg], r0 = p.grp.tile_r0[tg];
+    return GTileRows{r0, min(p.grp.off[e + 1], r0 + bn), e};
 }
 __device__ __forceinline__ int gact_row(const GemmP &p, int r) { return p.grouped && p.grp.amap ? p.grp.amap[r] : r; }
 __device__ __forceinline__ int gout_row(const GemmP &p, int r) { return p.grouped && p.grp.omap ? p.grp.omap[r] : r; }
@@ -93,7 +88,7 @@ constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, p
 
 template <int TY>
 struct GemmLds {
-    static constexpr int QB = TY == T_Q4_0 ? 16 : 32;  // weight code bytes per block in LDS
+    static constexpr int QB = 32;                       // weight codes per block in LDS: int8 (Q4_0 unpacked, −8 applied)
     static constexpr int WST = G_KC * QB + 16;          // weight row stride (bytes, padded)
 };
 
@@ -156,14 +151,20 @@ __device__ __forceinline__ void stage_store(GemmStage<TY, GLU, BN> &S, int tid, 
         uint8_t *wq = S.wq[nw] + row * WST + 2 * u * QB;
         float *dw = S.dw[nw] + row * G_KC + 2 * u;
         if constexpr (TY == T_Q4_0) {
-            uint4 q0, q1;
-            q0.x = __builtin_amdgcn_alignbyte(R.w.w[1], R.w.w[0], 2);
-            q0.y = __builtin_amdgcn_alignbyte(R.w.w[2], R.w.w[1], 2);
-            q0.z = __builtin_amdgcn_alignbyte(R.w.w[3], R.w.w[2], 2);
-            q0.w = __builtin_amdgcn_alignbyte(R.w.w[4], R.w.w[3], 2);
-            q1 = make_uint4(R.w.w[5], R.w.w[6], R.w.w[7], R.w.w[8]);
-            *(uint4 *)wq = q0;
-            *(uint4 *)(wq + 16) = q1;
+            // nibbles → int8 q − 8 once per workgroup: bytes 0..15 of a block are
+            // values 0..15 (low nibbles), bytes 16..31 values 16..31 (high nibbles)
+            uint32_t q[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(R.w.w[i + 1], R.w.w[i], 2);
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[4 + i] = R.w.w[5 + i];
+            auto lo8 = [](uint32_t v) { return ((v & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u; };
+            auto hi8 = [](uint32_t v) { return (((v >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u; };
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                *(uint4 *)(wq + 32 * b) = make_uint4(lo8(q[4 * b]), lo8(q[4 * b + 1]), lo8(q[4 * b + 2]), lo8(q[4 * b + 3]));
+                *(uint4 *)(wq + 32 * b + 16) = make_uint4(hi8(q[4 * b]), hi8(q[4 * b + 1]), hi8(q[4 * b + 2]), hi8(q[4 * b + 3]));
+            }
             dw[0] = h2f(R.w.w[0] & 0xffff);
             dw[1] = h2f(R.w.w[4] >> 16);
         } else {
@@ -194,8 +195,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * G_BM;
-    GTileRows tr;
-    if (!gtile_rows(p, tg, BN, tr)) return;  // whole workgroup: uniform
+    const GTileRows tr = gtile_rows(p, tg, BN);
+    if (tr.e < 0) return;  // whole workgroup: uniform
     const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
     const int tokA = gact_row(p, min(tr.r0 + tid / (256 / BN), tr.r_end - 1));
     const int tokD = gact_row(p, min(tr.r0 + tid % BN, tr.r_end - 1));
@@ -216,69 +217,81 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
     const v16i zi = {0};
     const v16f zf = {0};
 
+    // Stage ring: LDS holds stages s (being multiplied) and s + 1; two register sets
+    // hold the global loads of stages s + 1 and s + 2, so a stage's loads are issued
+    // two stages before their LDS store.  Load indices past the last stage repeat the
+    // last stage and the step count is even, so every load is unconditional and the
+    // compiler's wait for a register set counts exactly the loads issued after it.
     const int n_stages = p.K / (32 * G_KC);
-    StageRegs<TY, GLU, BN> R;
-    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, tid, R);
-    stage_store<TY, GLU, BN>(st[0], tid, R);
+    const int last_stage = n_stages - 1;
+    StageRegs<TY, GLU, BN> ra, rb;
+    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, tid, ra);
+    stage_store<TY, GLU, BN>(st[0], tid, ra);
+    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, min(1, last_stage) * G_KC, tid, rb);
     __syncthreads();
     // Per stage: all operands of the stage's KC blocks from LDS, then the
     // P = KC·NT·NW tile products in a software pipeline: the MFMAs of product
     // q+1 are issued before the VALU epilogue of product q.
     constexpr int P = G_KC * NT * NW;
-    for (int s = 0; s < n_stages; s++) {
-        const bool more = s + 1 < n_stages;
-        if (more) stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, (s + 1) * G_KC, tid, R);
-        const GemmStage<TY, GLU, BN> &S = st[s & 1];
-        v4i bw[G_KC][NW], av[G_KC][NT];
-        float bs[G_KC][NW], as[G_KC][NT];
+    // rl: receives stage s + 2; rs: holds stage s + 1, stored to LDS after stage s
+    auto body = [&](int s, StageRegs<TY, GLU, BN> &rl, const StageRegs<TY, GLU, BN> &rs) {
+        stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, min(s + 2, last_stage) * G_KC, tid, rl);
+        if (s < n_stages) {  // workgroup-uniform; the idle step of an odd stage count skips it
+            const GemmStage<TY, GLU, BN> &S = st[s & 1];
+            v4i bw[G_KC][NW], av[G_KC][NT];
+            float bs[G_KC][NW], as[G_KC][NT];
 #pragma unroll
-        for (int j = 0; j < G_KC; j++) {
+            for (int j = 0; j < G_KC; j++) {
 #pragma unroll
-            for (int a = 0; a < NW; a++) {
-                const uint4 q = *(const uint4 *)(S.wq[a] + wrow * WST + j * QB + (TY == T_Q4_0 ? 0 : 16 * h));
-                if constexpr (TY == T_Q4_0) {
-                    const uint32_t sh = 4u * (uint32_t)h;
-                    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) bw[j][a][i] = (int)((((qq[i] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
-                } else {
+                for (int a = 0; a < NW; a++) {
+                    const uint4 q = *(const uint4 *)(S.wq[a] + wrow * WST + j * QB + 16 * h);
                     bw[j][a] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                    bs[j][a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
                 }
-                bs[j][a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
-            }
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                av[j][t] = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
-                as[j][t] = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
+                for (int t = 0; t < NT; t++) {
+                    av[j][t] = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
+                    as[j][t] = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
+                }
+            }
+            v16i Iq[2];
+            v16f Sq[2];
+            // The MFMAs of product q take an (empty asm) dependency on the finished
+            // accumulators of product q-2: at most two result pairs are live, and the
+            // MFMAs of q overlap the VALU epilogue of q-1.
+            auto issue = [&](int q) {
+                const int j = q / (NT * NW), t = (q / NW) % NT, a = q % NW;
+                v4i aop = av[j][t];
+                if (q >= 2) {
+                    const int t2 = ((q - 2) / NW) % NT, a2 = (q - 2) % NW;
+                    const float *d = acc[a2][t2];
+                    asm volatile("" : "+v"(aop) : "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]), "v"(d[4]), "v"(d[5]), "v"(d[6]), "v"(d[7]),
+                                 "v"(d[8]), "v"(d[9]), "v"(d[10]), "v"(d[11]), "v"(d[12]), "v"(d[13]), "v"(d[14]), "v"(d[15]));
+                }
+                Iq[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bw[j][a], zi, 0, 0, 0);
+                Sq[q & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(as[j][t], bs[j][a], zf, 0, 0, 0);
+            };
+            issue(0);
+#pragma unroll
+            for (int q = 0; q < P; q++) {
+                if (q + 1 < P) issue(q + 1);
+                // scheduling fences: the epilogue of q stays between the MFMAs of q + 1 and
+                // those of q + 2, so it runs while the matrix core works on q + 1 (left to
+                // itself the scheduler moves each epilogue right behind its own MFMAs and
+                // fills the latency with s_nop)
+                __builtin_amdgcn_sched_barrier(0);
+                const int t = (q / NW) % NT, a = q % NW;
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)Iq[q & 1][v], Sq[q & 1][v], acc[a][t][v]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        v16i Iq[2];
-        v16f Sq[2];
-        // The MFMAs of product q take an (empty asm) dependency on the finished
-        // accumulators of product q-2: at most two result pairs are live, and the
-        // MFMAs of q overlap the VALU epilogue of q-1.
-        auto issue = [&](int q) {
-            const int j = q / (NT * NW), t = (q / NW) % NT, a = q % NW;
-            v4i aop = av[j][t];
-            if (q >= 2) {
-                const int t2 = ((q - 2) / NW) % NT, a2 = (q - 2) % NW;
-                const float *d = acc[a2][t2];
-                asm volatile("" : "+v"(aop) : "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]), "v"(d[4]), "v"(d[5]), "v"(d[6]), "v"(d[7]),
-                             "v"(d[8]), "v"(d[9]), "v"(d[10]), "v"(d[11]), "v"(d[12]), "v"(d[13]), "v"(d[14]), "v"(d[15]));
-            }
-            Iq[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bw[j][a], zi, 0, 0, 0);
-            Sq[q & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(as[j][t], bs[j][a], zf, 0, 0, 0);
-        };
-        issue(0);
-#pragma unroll
-        for (int q = 0; q < P; q++) {
-            if (q + 1 < P) issue(q + 1);
-            const int t = (q / NW) % NT, a = q % NW;
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)Iq[q & 1][v], Sq[q & 1][v], acc[a][t][v]);
-        }
-        if (more) stage_store<TY, GLU, BN>(st[(s + 1) & 1], tid, R);
+        if (s + 1 < n_stages) stage_store<TY, GLU, BN>(st[(s + 1) & 1], tid, rs);
         __syncthreads();
+    };
+    for (int s = 0; s < n_stages; s += 2) {
+        body(s, ra, rb);
+        body(s + 1, rb, ra);
     }
     // ---- epilogue: lane holds weight row row0 + wrow for tokens t0 + wc·64 + 32t + 16h + v ----
     const int rows = p.rows[sg];
@@ -307,12 +320,12 @@ bool gemm_supported(int ty, size_t K) {
 }
 
 // 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
-// then 64-token tiles (one 32-token tile per wave)
+// then 64-token tiles (one 32-token tile per wave); the gated pair always 64
 template <int TY, bool GLU>
 static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp) {
     const int slots = (p.n_rg + 7) / 8;
     int nt = 2;
-    if (slots * 8 * ((p.n_tok + 127) / 128) < 512 && p.n_tok > 64) nt = 1;
+    if (GLU || (slots * 8 * ((p.n_tok + 127) / 128) < 512 && p.n_tok > 64)) nt = 1;  // GLU: two register sets of 128-token stages do not fit
     p.n_tg = (p.n_tok + 64 * nt - 1) / (64 * nt);
     if (grp) {  // 64-token tiles from the grouping's table
         static_assert(GROUP_BN == 64, "grouped tiles are one 32-token tile per wave");
@@ -321,8 +334,13 @@ static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp) {
         p.grp = *grp;
         p.n_tg = grp->max_tiles;
     }
-    if (nt == 2) hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    if constexpr (!GLU) {
+        if (nt == 2) {
+            hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
 static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }

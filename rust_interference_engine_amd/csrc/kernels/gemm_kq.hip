@@ -62,22 +62,16 @@ constexpr int KQ_BM = 64, KQ_BN = 64;
 static_assert(KQ_BN == GROUP_BN, "grouped tiles are built for this token tile");
 
 // A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
-// [r0, r_end) of expert e (false: a tile past the grouping's count, nothing to do).
+// [r0, r_end) of expert e (e < 0: a tile past the grouping's count, nothing to
+// do).  Returned by value: the reference-parameter form kept it in scratch memory.
 struct TileRows {
     int r0, r_end, e;
 };
-__device__ __forceinline__ bool tile_rows(const KqP &p, int tg, TileRows &t) {
-    if (!p.grouped) {
-        t.r0 = tg * KQ_BN;
-        t.r_end = p.n_tok;
-        t.e = 0;
-        return true;
-    }
-    if (tg >= *p.grp.n_tiles) return false;
-    t.e = p.grp.tile_e[tg];
-    t.r0 = p.grp.tile_r0[tg];
-    t.r_end = min(p.grp.off[t.e + 1], t.r0 + KQ_BN);
-    return true;
+__device__ __forceinline__ TileRows tile_rows(const KqP &p, int tg) {
+    if (!p.grouped) return TileRows{tg * KQ_BN, p.n_tok, 0};
+    if (tg >= *p.grp.n_tiles) return TileRows{0, 0, -1};
+    const int e = p.grp.tile_e[tg], r0 = p.grp.tile_r0[tg];
+    return TileRows{r0, min(p.grp.off[e + 1], r0 + KQ_BN), e};
 }
 __device__ __forceinline__ int act_row(const KqP &p, int r) { return p.grouped && p.grp.amap ? p.grp.amap[r] : r; }
 __device__ __forceinline__ int out_row(const KqP &p, int r) { return p.grouped && p.grp.omap ? p.grp.omap[r] : r; }
@@ -189,8 +183,8 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
-    TileRows tr;
-    if (!tile_rows(p, tg, tr)) return;  // whole workgroup: uniform
+    const TileRows tr = tile_rows(p, tg);
+    if (tr.e < 0) return;  // whole workgroup: uniform
     const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
     const int tokA = act_row(p, min(tr.r0 + (tid >> 2), tr.r_end - 1));
     const int tokD = act_row(p, min(tr.r0 + (tid & 63), tr.r_end - 1));
@@ -371,8 +365,8 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
     const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
-    TileRows tr;
-    if (!tile_rows(p, tg, tr)) return;  // whole workgroup: uniform
+    const TileRows tr = tile_rows(p, tg);
+    if (tr.e < 0) return;  // whole workgroup: uniform
     const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
     const int tokA = act_row(p, min(tr.r0 + (tid >> 2), tr.r_end - 1));
     const int tokD = act_row(p, min(tr.r0 + (tid & 63), tr.r_end - 1));
