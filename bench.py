@@ -148,6 +148,9 @@ def main():
                                               "quantized hidden out)",
                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic() if args.workload == DEFAULT_WORKLOAD else None,
+                    "traffic_source": ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel, scaled by a 256 MiB copy: "
+                                       "profiles/gemv_dec_gate_up_glu_llama8b_q4_0_pmc.md (not measured in this run)")
+                    if args.workload == DEFAULT_WORKLOAD else None,
                     "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_us, 2)}
     prof = be.profile_decode(ctx_mid, reps=5)
     step_ms = sum(v[0] for v in prof.values()) / 5
