@@ -161,8 +161,8 @@ constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 // PRO8 (Q4_0/Q8_0 weights with a norm input): the activation is made in the
 // prologue; a separate instance, so that every load before the prologue is
 // unconditional and the compiler's wait for x does not cover the weight stream.
-template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false>
-__global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p) {  // 512 threads: two workgroups per CU
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8>
+__device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     static_assert(!PRO8 || TY == T_Q4_0 || TY == T_Q8_0, "the Q8_0 prologue serves Q4_0/Q8_0 weights");
     constexpr int GROUPS = NT / LPR;
     constexpr int STRIDE = LPR + DEC_PAD;
@@ -181,7 +181,6 @@ __global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p)
         uu[k] = valid[k] ? l + LPR * k : U - 1;  // idle lanes load a real unit and drop it
     }
     // workgroup → (segment, first row): uniform, so the segment's fields are scalar
-    const int bid = blockIdx.x;
     const int sg = (!GLU && p.nseg > 1 && bid >= p.blk_end[0]) ? ((p.nseg > 2 && bid >= p.blk_end[1]) ? 2 : 1) : 0;
     const int row0 = (bid - (sg ? p.blk_end[sg - 1] : 0)) * p.tr;
     const int seg_rows = p.seg[sg].rows;
@@ -510,21 +509,39 @@ __global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p)
     }
 }
 
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false>
+__global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p) {  // 512 threads: two workgroups per CU
+    dec_body<TY, LPR, UPL, GLU, R, NT, PRO8>(p, blockIdx.x);
+}
+
+// Q4_K and Q6_K segments of one activation in one launch (Q/K and V of a Q4_K_M
+// layer): the first n1 workgroups run the Q4_K rows, the others the Q6_K rows.
+// Each half is the single-type kernel's body with its own tile; with a norm input
+// both halves make the Q8_K activation in their prologue.
+template <int L1, int L2>
+__global__ __launch_bounds__(256) void gemv_dec_k46_kernel(DecP p1, DecP p2, int n1) {
+    if ((int)blockIdx.x < n1) dec_body<T_Q4_K, L1, 1, false, dec_rows_per_pass<T_Q4_K>(), 256, false>(p1, blockIdx.x);
+    else dec_body<T_Q6_K, L2, 1, false, dec_rows_per_pass<T_Q6_K>(), 256, false>(p2, blockIdx.x - n1);
+}
+
 static int dec_units(int ty, int K) {
     if (ty == T_Q6_K || ty == T_Q2_K || ty == T_Q3_K) return K / 32;
     if (ty == T_F32 || ty == T_F16 || ty == T_BF16) return K / 8;
     return K / 64;
 }
 
+// tile and grid of a decode GEMV launch: lanes per row, units per lane, threads,
+// LDS bytes and workgroups (p.tr and p.blk_end are filled in)
 template <int TY, int R>
-static bool launch_dec_r(DecP p, hipStream_t st) {
+static bool plan_dec(DecP &p, int &lpr, int &upl, int &nt, size_t &lds, int &blocks) {
     const int U = dec_units(TY, p.K);
-    int lpr = 16;
+    lpr = 16;
     while (lpr < U && lpr < 256) lpr *= 2;
-    const int upl = (U + lpr - 1) / lpr;
+    upl = (U + lpr - 1) / lpr;
     if (upl > 2) return false;
     int pass = (256 / lpr) * R;  // rows per pass of a 256-thread workgroup
-    int m, nt = 256;
+    int m;
+    nt = 256;
     if (p.glu && p.hq.qs) {
         if (p.total_rows % 32) return false;
         // whole Q8_0 blocks of h per workgroup, in one pass: 512 or 1024 threads
@@ -542,14 +559,22 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         p.tr = pass;
         if (p.slot_rows % p.tr || (p.glu && p.hq.qs && p.tr % 32)) return false;
     }
-    const size_t lds = ((size_t)(p.glu ? 2 : 1) * p.tr * (lpr + DEC_PAD) + p.tr) * sizeof(float);
+    lds = ((size_t)(p.glu ? 2 : 1) * p.tr * (lpr + DEC_PAD) + p.tr) * sizeof(float);
     if (lds > 64 * 1024) return false;
-    int blocks = 0;
+    blocks = 0;
     const int nseg = p.glu ? 1 : p.nseg;
     for (int i = 0; i < 3; i++) {
         if (i < nseg) blocks += (p.seg[i].rows + p.tr - 1) / p.tr;
         p.blk_end[i] = blocks;
     }
+    return true;
+}
+
+template <int TY, int R>
+static bool launch_dec_r(DecP p, hipStream_t st) {
+    int lpr, upl, nt, blocks;
+    size_t lds;
+    if (!plan_dec<TY, R>(p, lpr, upl, nt, lds, blocks)) return false;
     constexpr bool Q8PRO = TY == T_Q4_0 || TY == T_Q8_0;
     const bool pro = Q8PRO && p.nin.x;
 #define RIE_DEC_P(L, UP, PR)                                                                                          \
@@ -582,6 +607,24 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
 #undef RIE_DEC
 #undef RIE_DEC_P
     return true;
+}
+
+// Q4_K segments (p1) and Q6_K segments (p2) of one activation in one launch
+static bool launch_dec_k46(DecP p1, DecP p2, hipStream_t st) {
+    int l1, u1, n1t, b1, l2, u2, n2t, b2;
+    size_t lds1, lds2;
+    if (!plan_dec<T_Q4_K, dec_rows_per_pass<T_Q4_K>()>(p1, l1, u1, n1t, lds1, b1) ||
+        !plan_dec<T_Q6_K, dec_rows_per_pass<T_Q6_K>()>(p2, l2, u2, n2t, lds2, b2))
+        return false;
+    if (u1 != 1 || u2 != 1 || n1t != 256 || n2t != 256 || l2 != 2 * l1) return false;
+    const size_t lds = std::max(lds1, lds2);
+    const dim3 grid(b1 + b2), block(256);
+    switch (l1) {
+    case 32: hipLaunchKernelGGL((gemv_dec_k46_kernel<32, 64>), grid, block, lds, st, p1, p2, b1); return true;
+    case 64: hipLaunchKernelGGL((gemv_dec_k46_kernel<64, 128>), grid, block, lds, st, p1, p2, b1); return true;
+    case 128: hipLaunchKernelGGL((gemv_dec_k46_kernel<128, 256>), grid, block, lds, st, p1, p2, b1); return true;
+    default: return false;
+    }
 }
 
 template <int TY>
@@ -688,6 +731,31 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
     if (nin && (n_tok != 1 || !nin->x || !nin->w)) return false;
     for (int s = 0; s < nseg; s++)
         if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K) && !gemv_norm_f32_ok(segs[s].w.ty, (size_t)K)) return false;
+    // one token, Q4_K segments followed by Q6_K ones (the Q4_K_M attention): one launch
+    if (n_tok == 1 && nseg >= 2) {
+        int k = 0;
+        while (k < nseg && segs[k].w.ty == T_Q4_K) k++;
+        bool mixed = k > 0 && k < nseg;
+        for (int s = k; s < nseg; s++) mixed = mixed && segs[s].w.ty == T_Q6_K;
+        for (int s = 0; s < nseg && mixed; s++)
+            mixed = gemv_supported(segs[s].w.ty, K) && segs[s].w.cols == (size_t)K && segs[s].w.data && segs[s].out &&
+                    operands_ok(segs[s].w.ty, act, act_f32);
+        if (mixed) {
+            DecP d[2]{};
+            for (int s = 0; s < nseg; s++) {
+                DecP &dd = d[s < k ? 0 : 1];
+                dd.seg[dd.nseg++] = SegP{segs[s].w.data, segs[s].w.rb(), (int)segs[s].w.rows, segs[s].out, segs[s].ld, segs[s].epi};
+                dd.total_rows += (int)segs[s].w.rows;
+            }
+            for (auto &dd : d) {
+                dd.K = K;
+                dd.act = act;
+                dd.actf = act_f32;
+                if (nin) dd.nin = *nin;
+            }
+            if (launch_dec_k46(d[0], d[1], st)) return true;
+        }
+    }
     // segments of one launch must share a weight type; split otherwise
     int i = 0;
     while (i < nseg) {
