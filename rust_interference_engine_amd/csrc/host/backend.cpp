@@ -486,11 +486,19 @@ void HipBackend::run_layers(int n, size_t pos0, const int *d_pos0, bool all_logi
             cap_[2][il].resize((size_t)n * qd);
             RIE_HIP_CHECK(hipMemcpy(cap_[2][il].data(), d_att_, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
         }
-        if (wo_fmt == ACT_Q8K) launch_quant_only(d_att_, qd, n, qd, ACT_Q8K, actk_, st_);
+        // one token, K-quant wo: its GEMV quantizes the attention output itself (Q8_K prologue without a norm)
+        const bool wo_self_q = n == 1 && !capture_ && wo_fmt == ACT_Q8K && gemv_norm_ok(L.wo.ty, qd);
+        if (wo_fmt == ACT_Q8K && !wo_self_q) launch_quant_only(d_att_, qd, n, qd, ACT_Q8K, actk_, st_);
         if (wo_fmt == ACT_F32) RIE_HIP_CHECK(hipMemcpyAsync(d_xn_, d_att_, (size_t)n * qd * 4, hipMemcpyDeviceToDevice, st_));
         const bool direct = !L.post_attn_norm && c.residual_scale == 1.0f;
         GemvSeg so{L.wo, direct ? d_x_ : d_o_, E, direct ? EPI_ADD : EPI_STORE};
-        matmul(&so, 1, n, qd);
+        if (wo_self_q) {
+            const NormIn qin{d_att_, nullptr, 0.0f, 0};
+            if (!launch_gemv(&so, 1, actk_, d_xn_, 1, qd, st_, &qin)) throw rt_err("quantizing wo GEMV launch failed");
+            check_launch("matmul");
+        } else {
+            matmul(&so, 1, n, qd);
+        }
         mark("matmul_wo");
         if (!direct) {
             if (L.post_attn_norm) launch_rmsnorm(d_o_, E, L.post_attn_norm, c.rms_eps, n, E, d_o_, E, 1, st_);

@@ -27,7 +27,8 @@ struct GemvSeg {
 // y_seg = W_seg · act for up to 3 segments sharing one activation batch (n_tok rows).
 // Returns false when a weight type/shape has no kernel.
 // nin (single token, Q4_0/Q8_0 weights, K ≤ 4096): the kernel computes the
-// activation itself as Q8_0(RMSNorm(x)·w) — no separate normalization launch.
+// activation itself as Q8_0(RMSNorm(x)·w) — no separate normalization launch;
+// K-quant weights likewise as Q8_K, and with nin->w == nullptr as Q8_K(x).
 struct NormIn {
     const float *x;   // residual row [K]
     const float *w;   // norm weight [K]

@@ -728,9 +728,12 @@ bool gemv_norm_f32_ok(int ty, size_t K) { return ty == T_F32 && K % 16 == 0 && K
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
                  const NormIn *nin) {
     if (n_tok < 1) return false;
-    if (nin && (n_tok != 1 || !nin->x || !nin->w)) return false;
-    for (int s = 0; s < nseg; s++)
+    if (nin && (n_tok != 1 || !nin->x)) return false;
+    for (int s = 0; s < nseg; s++) {
         if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K) && !gemv_norm_f32_ok(segs[s].w.ty, (size_t)K)) return false;
+        // without a norm weight only the Q8_K prologue applies (it then quantizes x as it is)
+        if (nin && !nin->w && act_format(segs[s].w.ty) != ACT_Q8K) return false;
+    }
     // one token, Q4_K segments followed by Q6_K ones (the Q4_K_M attention): one launch
     if (n_tok == 1 && nseg >= 2) {
         int k = 0;
