@@ -40,6 +40,8 @@ struct NormIn {
     int order16;
 };
 bool gemv_norm_ok(int ty, size_t K);
+// K-quant weights with nin->w == nullptr: the prologue quantizes x to Q8_K (K ≤ 8192)
+bool gemv_quant_ok(int ty, size_t K);
 // F32 weights with nin: the activation is RMSNorm(x)·w in f32, equal to the standalone norm's rows
 bool gemv_norm_f32_ok(int ty, size_t K);
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,

@@ -158,12 +158,62 @@ constexpr int DEC_PAD = 8;  // LDS row padding of the partial-sum tile
 
 // NT threads (256 or 512): one pass of NT/LPR row groups × R rows covers a
 // 32-row tile in a single pass (all of a workgroup's loads issued up front).
+// One 16-value group gi of a Q8_K superblock (the 16 lanes of a 16-lane row hold
+// one superblock): the superblock's first strictly largest |y| (DPP within the
+// row, the lower index winning ties), iscale = −127/max, round-half-away codes,
+// the group's sum, d = 1/iscale (quant/mod.rs:191-218).  Writes the codes, the
+// group sum and (first lane of the row) d into the LDS copy of the activation.
+__device__ __forceinline__ void q8k_group_to_lds(const float (&y)[16], int gi, int8_t *s_q, int16_t *s_bs, float *s_d) {
+    float am = 0.0f, mv = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        if (fabsf(y[e]) > am) {
+            am = fabsf(y[e]);
+            mv = y[e];
+            idx = 16 * gi + e;
+        }
+    auto merge = [&](float oa, float om, int oi) {
+        if (oa > am || (oa == am && oi < idx)) {
+            am = oa;
+            mv = om;
+            idx = oi;
+        }
+    };
+    merge(dpp_f<DPP_QUAD_XOR1>(am), dpp_f<DPP_QUAD_XOR1>(mv), dpp_i<DPP_QUAD_XOR1>(idx));
+    merge(dpp_f<DPP_QUAD_XOR2>(am), dpp_f<DPP_QUAD_XOR2>(mv), dpp_i<DPP_QUAD_XOR2>(idx));
+    merge(dpp_f<DPP_ROW_ROR4>(am), dpp_f<DPP_ROW_ROR4>(mv), dpp_i<DPP_ROW_ROR4>(idx));
+    merge(dpp_f<DPP_ROW_ROR8>(am), dpp_f<DPP_ROW_ROR8>(mv), dpp_i<DPP_ROW_ROR8>(idx));
+    uint32_t w4[4] = {0u, 0u, 0u, 0u};
+    int bsum = 0;
+    float dsb = 0.0f;
+    if (am != 0.0f) {
+        const float iscale = -127.0f / mv;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            int q = (int)roundf(iscale * y[e]);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            bsum += q;
+            w4[e >> 2] |= ((uint32_t)(q & 0xff)) << (8 * (e & 3));
+        }
+        dsb = 1.0f / iscale;
+    }
+    *(uint4 *)(s_q + 16 * gi) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    s_bs[gi] = (int16_t)bsum;
+    if ((gi & 15) == 0) s_d[gi >> 4] = dsb;
+}
+constexpr int QK_PRO_MAX = 8192;  // widest activation the quantize-only Q8_K prologue holds in LDS
+
 // PRO8 (Q4_0/Q8_0 weights with a norm input): the activation is made in the
 // prologue; a separate instance, so that every load before the prologue is
 // unconditional and the compiler's wait for x does not cover the weight stream.
-template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8>
+// PROQ (K-quant weights, an activation to quantize without a norm): the same for
+// Q8_K(x), widths up to QK_PRO_MAX.
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8, bool PROQ = false>
 __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     static_assert(!PRO8 || TY == T_Q4_0 || TY == T_Q8_0, "the Q8_0 prologue serves Q4_0/Q8_0 weights");
+    static_assert(!PROQ || ((TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K) && !GLU),
+                  "the quantize-only prologue serves K-quant weights");
     constexpr int GROUPS = NT / LPR;
     constexpr int STRIDE = LPR + DEC_PAD;
     constexpr int NW = GLU ? 2 : 1;
@@ -227,7 +277,21 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
             }
         }
         load_pass(base0);  // unconditional (rows are clamped): a group without rows here drops its loads
-    } else {
+    }
+    constexpr int QG = PROQ ? (QK_PRO_MAX / 16 + NT - 1) / NT : 1;  // PROQ: 16-value groups per thread
+    float4 xq[QG][4];  // PROQ: groups τ + NT·g of x
+    if constexpr (PROQ) {
+        const float *xr = p.nin.x + ((p.xsel && p.act_per_slot) ? (size_t)slot * p.K : 0);
+#pragma unroll
+        for (int g = 0; g < QG; g++) {
+            const int gi = tid + NT * g;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                xq[g][i] = gi < (p.K >> 4) ? ((const float4 *)(xr + 16 * gi))[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        load_pass(base0);  // unconditional, as above
+    }
+    if constexpr (!PRO8 && !PROQ) {
         if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
     }
     bool have_act = false;
@@ -310,6 +374,38 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
             }
             have_act = true;
         }
+    } else if constexpr (PROQ) {
+        // Q8_K(x) of the whole activation in LDS, groups quantized as the standalone
+        // quantizer does (q8k_group_to_lds); LDS-only barriers, as in PRO8
+        __shared__ __align__(16) int8_t s_qk[QK_PRO_MAX];
+        __shared__ float s_dk[QK_PRO_MAX / 256];
+        __shared__ __align__(16) int16_t s_bsk[QK_PRO_MAX / 16];
+        const int K = p.K;
+        lds_barrier();  // the previous workgroup-local use of the LDS copy is over
+#pragma unroll
+        for (int g = 0; g < QG; g++) {
+            const int gi = tid + NT * g;
+            if (gi < (K >> 4)) {  // whole 16-lane rows (K % 256 == 0)
+                float y[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    y[4 * i] = xq[g][i].x;
+                    y[4 * i + 1] = xq[g][i].y;
+                    y[4 * i + 2] = xq[g][i].z;
+                    y[4 * i + 3] = xq[g][i].w;
+                }
+                q8k_group_to_lds(y, gi, s_qk, s_bsk, s_dk);
+            }
+        }
+        lds_barrier();
+        ActQ8 la;
+        la.qs = s_qk;
+        la.d = s_dk;
+        la.bsums = s_bsk;
+#pragma unroll
+        for (int k = 0; k < UPL; k++)
+            if (valid[k]) load_act<TY>(a[k], uu[k], la, nullptr, K, 0);
+        have_act = true;
     } else if constexpr (TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K) {
         if (p.nin.x) {
             // The activation is Q8_K(RMSNorm(x)·w), made here once per workgroup in
@@ -353,43 +449,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
                     y[4 * i + 2] = xv.z * scale * gv.z;
                     y[4 * i + 3] = xv.w * scale * gv.w;
                 }
-                float am = 0.0f, mv = 0.0f;
-                int idx = 0x7fffffff;
-#pragma unroll
-                for (int e = 0; e < 16; e++)
-                    if (fabsf(y[e]) > am) {
-                        am = fabsf(y[e]);
-                        mv = y[e];
-                        idx = 16 * tid + e;
-                    }
-                auto merge = [&](float oa, float om, int oi) {
-                    if (oa > am || (oa == am && oi < idx)) {
-                        am = oa;
-                        mv = om;
-                        idx = oi;
-                    }
-                };
-                merge(dpp_f<DPP_QUAD_XOR1>(am), dpp_f<DPP_QUAD_XOR1>(mv), dpp_i<DPP_QUAD_XOR1>(idx));
-                merge(dpp_f<DPP_QUAD_XOR2>(am), dpp_f<DPP_QUAD_XOR2>(mv), dpp_i<DPP_QUAD_XOR2>(idx));
-                merge(dpp_f<DPP_ROW_ROR4>(am), dpp_f<DPP_ROW_ROR4>(mv), dpp_i<DPP_ROW_ROR4>(idx));
-                merge(dpp_f<DPP_ROW_ROR8>(am), dpp_f<DPP_ROW_ROR8>(mv), dpp_i<DPP_ROW_ROR8>(idx));
-                uint32_t w4[4] = {0u, 0u, 0u, 0u};
-                int bsum = 0;
-                float dsb = 0.0f;
-                if (am != 0.0f) {
-                    const float iscale = -127.0f / mv;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        int q = (int)roundf(iscale * y[e]);
-                        q = q < -127 ? -127 : (q > 127 ? 127 : q);
-                        bsum += q;
-                        w4[e >> 2] |= ((uint32_t)(q & 0xff)) << (8 * (e & 3));
-                    }
-                    dsb = 1.0f / iscale;
-                }
-                *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-                s_bs[tid] = (int16_t)bsum;
-                if ((tid & 15) == 0) s_d[tid >> 4] = dsb;
+                q8k_group_to_lds(y, tid, s_q, s_bs, s_d);
             }
             __syncthreads();
             ActQ8 la;
@@ -509,9 +569,9 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     }
 }
 
-template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false>
+template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false, bool PROQ = false>
 __global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p) {  // 512 threads: two workgroups per CU
-    dec_body<TY, LPR, UPL, GLU, R, NT, PRO8>(p, blockIdx.x);
+    dec_body<TY, LPR, UPL, GLU, R, NT, PRO8, PROQ>(p, blockIdx.x);
 }
 
 // Q4_K and Q6_K segments of one activation in one launch (Q/K and V of a Q4_K_M
@@ -576,7 +636,9 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
     size_t lds;
     if (!plan_dec<TY, R>(p, lpr, upl, nt, lds, blocks)) return false;
     constexpr bool Q8PRO = TY == T_Q4_0 || TY == T_Q8_0;
+    constexpr bool KPRO = TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K;
     const bool pro = Q8PRO && p.nin.x;
+    const bool proq = KPRO && p.nin.x && !p.nin.w && !p.glu && nt == 256 && upl == 1 && lpr >= 32 && p.K <= QK_PRO_MAX;
 #define RIE_DEC_P(L, UP, PR)                                                                                          \
     do {                                                                                                              \
         if (p.glu && nt == 512) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 512, PR>), dim3(blocks), dim3(512), lds, st, p);    \
@@ -584,14 +646,17 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         else if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);      \
         else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);                \
     } while (0)
-#define RIE_DEC(L, UP)                           \
-    do {                                         \
-        if constexpr (Q8PRO) {                   \
-            if (pro) RIE_DEC_P(L, UP, true);     \
-            else RIE_DEC_P(L, UP, false);        \
-        } else {                                 \
-            RIE_DEC_P(L, UP, false);             \
-        }                                        \
+#define RIE_DEC(L, UP)                                                                                                  \
+    do {                                                                                                                \
+        if constexpr (Q8PRO) {                                                                                          \
+            if (pro) RIE_DEC_P(L, UP, true);                                                                            \
+            else RIE_DEC_P(L, UP, false);                                                                               \
+        } else if constexpr (KPRO && UP == 1 && L >= 32) {                                                              \
+            if (proq) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, 1, false, R, 256, false, true>), dim3(blocks), dim3(256), lds, st, p); \
+            else RIE_DEC_P(L, UP, false);                                                                               \
+        } else {                                                                                                        \
+            RIE_DEC_P(L, UP, false);                                                                                    \
+        }                                                                                                               \
     } while (0)
     if (upl == 1) {
         switch (lpr) {
@@ -725,14 +790,19 @@ bool gemv_norm_ok(int ty, size_t K) {
 
 bool gemv_norm_f32_ok(int ty, size_t K) { return ty == T_F32 && K % 16 == 0 && K >= 16; }
 
+bool gemv_quant_ok(int ty, size_t K) {
+    return (ty == T_Q2_K || ty == T_Q3_K || ty == T_Q4_K || ty == T_Q5_K || ty == T_Q6_K) && K % 256 == 0 && K >= 256 &&
+           K <= (size_t)QK_PRO_MAX;
+}
+
 bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *act_f32, int n_tok, int K, hipStream_t st,
                  const NormIn *nin) {
     if (n_tok < 1) return false;
     if (nin && (n_tok != 1 || !nin->x)) return false;
     for (int s = 0; s < nseg; s++) {
-        if (nin && !gemv_norm_ok(segs[s].w.ty, (size_t)K) && !gemv_norm_f32_ok(segs[s].w.ty, (size_t)K)) return false;
+        if (nin && nin->w && !gemv_norm_ok(segs[s].w.ty, (size_t)K) && !gemv_norm_f32_ok(segs[s].w.ty, (size_t)K)) return false;
         // without a norm weight only the Q8_K prologue applies (it then quantizes x as it is)
-        if (nin && !nin->w && act_format(segs[s].w.ty) != ACT_Q8K) return false;
+        if (nin && !nin->w && !gemv_quant_ok(segs[s].w.ty, (size_t)K)) return false;
     }
     // one token, Q4_K segments followed by Q6_K ones (the Q4_K_M attention): one launch
     if (n_tok == 1 && nseg >= 2) {
@@ -800,7 +870,9 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
                          const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st, const NormIn *nin) {
     // with nin: the K-quant prologue quantizes (and with nin->w normalizes) the activation itself
-    if (nin && (!nin->x || act_format(stacked.ty) != ACT_Q8K || !gemv_norm_ok(stacked.ty, (size_t)K))) return false;
+    if (nin && (!nin->x || act_format(stacked.ty) != ACT_Q8K ||
+                !(nin->w ? gemv_norm_ok(stacked.ty, (size_t)K) : gemv_quant_ok(stacked.ty, (size_t)K))))
+        return false;
     if (!gemv_supported(stacked.ty, (size_t)K) || stacked.cols != (size_t)K || !stacked.data || !out || !sel || n_slots < 1 ||
         slot_rows < 1 || stacked.rows % (size_t)slot_rows || !operands_ok(stacked.ty, act, act_f32))
         return false;
