@@ -223,6 +223,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     part_floats_ = (size_t)std::max<size_t>(32 * mb, ATT_MAX_SPLIT) * c.n_head * (hd + 2);
     d_part_ = dalloc<float>(allocs_, part_floats_);
     d_attn_cnt_ = dalloc<int>(allocs_, c.n_head * ATT_CNT_STRIDE);  // one per head slice: at most one per query head
+    d_route_cnt_ = dalloc<int>(allocs_, 64);  // the router GEMV's arrival counter (one-token routing)
     d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
     if (c.n_expert) {
@@ -627,7 +628,20 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
     }
     mark("rmsnorm_quant");
     GemvSeg rs{L.router, d_router_, ne, EPI_STORE};
-    if (self_norm) {
+    // one token, F32 router: its last workgroup also routes the token (no routing launch)
+    RouteEpi re;
+    re.cnt = d_route_cnt_;
+    re.n_exp = ne;
+    re.k = k;
+    re.norm_topk = L.norm_topk;
+    re.unit_weights = L.unit_weights;
+    re.sel = d_moe_sel_;
+    re.wgt = d_moe_w_;
+    const bool routed = n == 1 && !capture_ &&
+                        launch_gemv_route(rs, act_format(L.router.ty) == ACT_Q8K ? actk_ : act0_, d_xn_, E, self_norm ? &nin : nullptr, re, st_);
+    if (routed) {
+        check_launch("router");
+    } else if (self_norm) {
         if (!launch_gemv(&rs, 1, act_format(L.router.ty) == ACT_Q8K ? actk_ : act0_, d_xn_, 1, E, st_, &nin))
             throw rt_err("normalizing router GEMV launch failed");
     } else {
@@ -639,7 +653,7 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
         cap_[7][cur_layer_].resize((size_t)n * ne);
         RIE_HIP_CHECK(hipMemcpy(cap_[7][cur_layer_].data(), d_router_, (size_t)n * ne * 4, hipMemcpyDeviceToHost));
     }
-    launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
+    if (!routed) launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
     check_launch("moe route");
     mark("moe_route");
     if (!self_norm) RIE_HIP_CHECK(hipMemcpyAsync(d_moe_xn_, d_xn_, (size_t)n * E * 4, hipMemcpyDeviceToDevice, st_));

@@ -128,6 +128,7 @@ class HipBackend {
           *d_o_ = nullptr, *d_logits_ = nullptr, *d_part_ = nullptr, *d_amax_val_ = nullptr, *d_gemm_ws_ = nullptr;
     int *d_amax_idx_ = nullptr;
     int *d_attn_cnt_ = nullptr;  // per-KV-head arrival counters of the fused single-token attention
+    int *d_route_cnt_ = nullptr;  // arrival counter of the router GEMV that routes one token
     ActQ8 act0_, actk_;  // Q8_0 and Q8_K batches
     ActQ8 act_h_;        // Q8_0 of the single-token FFN hidden
     size_t kmax_ = 0, ff_max_ = 0, part_floats_ = 0;

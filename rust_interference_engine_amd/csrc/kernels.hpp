@@ -52,6 +52,16 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
 bool launch_gemv_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, const float *act_f32, int n_tok, int K, float *h,
                      int ld, int gelu, const ActQ8 *hq, hipStream_t st, const NormIn *nin = nullptr);
 bool gemv_supported(int ty, size_t K);
+// Routing of one token by the router GEMV's last workgroup (F32 router weights):
+// the logits go to seg.out as usual, then sel/wgt receive the token's top-k
+// (the routing kernel's results).  cnt: one int, zero before the first launch,
+// re-armed by each launch.  False (nothing launched) when not applicable.
+struct RouteEpi {
+    int *cnt = nullptr;
+    int n_exp = 0, k = 0, norm_topk = 0, unit_weights = 0;
+    int *sel = nullptr;
+    float *wgt = nullptr;
+};
 
 // ---- attention.hip ----
 struct HeadPrepArgs {
@@ -134,6 +144,8 @@ void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *
 // when act_per_slot); the GLU variant writes h [n_slots][ff].
 // With nin (Q8_K weight types): every workgroup quantizes its activation row from
 // nin->x itself (normalized first when nin->w is given).
+bool launch_gemv_route(const GemvSeg &seg, const ActQ8 &act, const float *act_f32, int K, const NormIn *nin, const RouteEpi &route,
+                       hipStream_t st);
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,
                          const float *act_f32, bool act_per_slot, int K, float *out, hipStream_t st,
                          const NormIn *nin = nullptr);

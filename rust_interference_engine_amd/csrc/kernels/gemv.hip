@@ -16,6 +16,7 @@
 #include "../common.hpp"
 #include "../device.hpp"
 #include "../kernels.hpp"
+#include "../moe_route.hpp"
 #include "../gemv_units.hpp"
 
 #include <algorithm>
@@ -68,6 +69,7 @@ struct DecP {
     const int *xsel;
     int slot_rows;
     int act_per_slot;  // slot j reads activation row j (the down projection of expert j's hidden)
+    RouteEpi route;    // F32 router of one token: the last workgroup routes it (route.cnt != nullptr)
 };
 
 // ---------------------------------------------------------------------------
@@ -569,9 +571,32 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     }
 }
 
+// The router GEMV's last workgroup routes the token: every workgroup counts its
+// stored logits with an agent-scope release; the last one to arrive takes an
+// agent-scope acquire, re-arms the counter and runs the routing in its first wave.
+__device__ __forceinline__ void route_last_workgroup(const DecP &p) {
+    __shared__ int s_last;
+    __shared__ __align__(16) float s_ps[64 * 8];
+    __syncthreads();  // the workgroup's logits are stored
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(p.route.cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (int)gridDim.x - 1;
+        if (s_last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __hip_atomic_store(p.route.cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    if (s_last && threadIdx.x < 64)
+        moe_route_wave(p.seg[0].out, p.route.n_exp, p.route.k, p.route.norm_topk, p.route.unit_weights, p.route.sel, p.route.wgt, s_ps);
+}
+
 template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false, bool PROQ = false>
 __global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p) {  // 512 threads: two workgroups per CU
     dec_body<TY, LPR, UPL, GLU, R, NT, PRO8, PROQ>(p, blockIdx.x);
+    if constexpr (TY == T_F32 && !GLU) {
+        if (p.route.cnt) route_last_workgroup(p);
+    }
 }
 
 // Q4_K and Q6_K segments of one activation in one launch (Q/K and V of a Q4_K_M
@@ -865,6 +890,26 @@ bool launch_gemv(const GemvSeg *segs, int nseg, const ActQ8 &act, const float *a
         i = j;
     }
     return true;
+}
+
+bool launch_gemv_route(const GemvSeg &seg, const ActQ8 &act, const float *act_f32, int K, const NormIn *nin, const RouteEpi &route,
+                       hipStream_t st) {
+    // F32 router weights only (the instances that carry the routing epilogue); n_exp ≤ 512
+    if (seg.w.ty != T_F32 || !route.cnt || !route.sel || !route.wgt || route.n_exp < 1 || route.n_exp > 512 || route.k < 1 ||
+        route.k > route.n_exp || route.k > 64 || seg.w.rows != (size_t)route.n_exp || seg.epi != EPI_STORE ||
+        !gemv_supported(seg.w.ty, K) || seg.w.cols != (size_t)K || !seg.w.data || !seg.out)
+        return false;
+    if (nin && (!nin->x || !nin->w || !gemv_norm_f32_ok(seg.w.ty, (size_t)K))) return false;
+    DecP d{};
+    d.seg[0] = SegP{seg.w.data, seg.w.rb(), (int)seg.w.rows, seg.out, seg.ld, EPI_STORE};
+    d.nseg = 1;
+    d.total_rows = (int)seg.w.rows;
+    d.K = K;
+    d.act = act;
+    d.actf = act_f32;
+    if (nin) d.nin = *nin;
+    d.route = route;
+    return dispatch_dec(T_F32, d, st);
 }
 
 bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel, int n_slots, const ActQ8 &act,

@@ -1,6 +1,7 @@
 // misc.hip — greedy argmax, elementwise epilogues and MoE routing for gfx950.
 #include "../common.hpp"
 #include "../device.hpp"
+#include "../moe_route.hpp"
 #include "../kernels.hpp"
 
 #include <algorithm>
@@ -154,93 +155,12 @@ void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, cons
     launch_rmsnorm_quant(x, ldx, nullptr, 0.0f, n_rows, K, nullptr, fmt, act, st);
 }
 
-// MoE routing (model/cpu.rs:487-501): softmax over the router logits, sort by
-// probability descending with the lower expert index first on ties, keep the
-// top k, optionally renormalize by their sum taken in sorted order.
-// One wave per token: lane l holds experts l + 64i (n_exp ≤ 512, checked by the
-// host).  The softmax sum runs over the experts in order, sequentially, like the
-// reference's (ops.rs:38-49), by one lane over an LDS copy.  Top-k is k rounds:
-// the maximum of the experts not yet taken (DPP within 16-lane rows, then the
-// four row maxima), and of the experts holding it the lowest index (ballots in
-// expert order), which is the reference's index tie-break (cpu.rs:495).  Lane j
-// keeps the j-th choice and writes it at its rank in ascending expert order (the
-// CPU path adds the experts' outputs in that order, cpu.rs:502-513, and so does
-// launch_moe_combine).
-__device__ __forceinline__ float row_max16(float v) {
-    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
-    v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
-    v = fmaxf(v, dpp_f<DPP_ROW_ROR4>(v));
-    return fmaxf(v, dpp_f<DPP_ROW_ROR8>(v));
-}
+// MoE routing: one wavefront per token (moe_route_wave, moe_route.hpp)
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_exp, int k, int norm_topk, int unit_weights, int *sel,
                                                        float *wgt) {
-    constexpr int NE = 8;
-    __shared__ __align__(16) float ps[64 * NE];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *l = logits + (size_t)t * n_exp;
-    float pr[NE];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int e = lane + 64 * i;
-        pr[i] = e < n_exp ? l[e] : -INFINITY;
-        mx = fmaxf(mx, pr[i]);
-    }
-    mx = wave_max(mx, 64);
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        pr[i] = lane + 64 * i < n_exp ? expf(pr[i] - mx) : 0.0f;
-        ps[lane + 64 * i] = pr[i];
-    }
-    __syncthreads();
-    __shared__ float s_inv;
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int e0 = 0; e0 < n_exp; e0 += 4) {  // n_exp % 4 == 0 is not assumed: the pad holds zeros
-            const float4 q = *(const float4 *)(ps + e0);
-            sum += q.x;
-            if (e0 + 1 < n_exp) sum += q.y;
-            if (e0 + 2 < n_exp) sum += q.z;
-            if (e0 + 3 < n_exp) sum += q.w;
-        }
-        s_inv = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = s_inv;
-#pragma unroll
-    for (int i = 0; i < NE; i++) pr[i] *= inv;
-    uint32_t taken = 0;  // bit i: expert lane + 64i is chosen
-    int my_c = 0x7fffffff;
-    float my_v = 0.0f, norm = 0.0f;
-    for (int j = 0; j < k; j++) {
-        float v = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < NE; i++)
-            if (lane + 64 * i < n_exp && !((taken >> i) & 1u)) v = fmaxf(v, pr[i]);
-        v = row_max16(v);
-        const auto rl = [&](int ln) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), ln)); };
-        const float m = fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));  // the row maxima
-        int idx = 0x7fffffff;
-#pragma unroll
-        for (int i = NE - 1; i >= 0; i--) {  // the lowest expert index holding m
-            const bool cand = lane + 64 * i < n_exp && !((taken >> i) & 1u) && pr[i] == m;
-            const uint64_t b = __ballot(cand);
-            if (b) idx = 64 * i + __builtin_ctzll(b);
-        }
-        if (idx < n_exp && (idx & 63) == lane) taken |= 1u << (idx >> 6);
-        if (lane == j) {
-            my_c = idx;
-            my_v = m;
-        }
-        norm += m;  // in choice order
-    }
-    if (!norm_topk) norm = 1.0f;
-    int rank = 0;
-    for (int q = 0; q < k; q++) rank += __builtin_amdgcn_readlane(my_c, q) < my_c;
-    if (lane < k) {
-        sel[(size_t)t * k + rank] = my_c;
-        wgt[(size_t)t * k + rank] = unit_weights ? 1.0f : my_v / norm;
-    }
+    __shared__ __align__(16) float ps[64 * 8];
+    const size_t t = blockIdx.x;
+    moe_route_wave(logits + t * n_exp, n_exp, k, norm_topk, unit_weights, sel + t * k, wgt + t * k, ps);
 }
 
 // out[t] (= or +=) Σ_j w[t][j]·y[t·k + j], j in ascending expert order, starting from 0
