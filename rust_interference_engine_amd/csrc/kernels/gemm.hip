@@ -4,7 +4,8 @@
 //
 // One wavefront computes 32 weight rows × 32·NT tokens.  Per 32-value block b:
 //   I[t][r]  = Σ_k a_q[t][k]·(w_q[r][k] − 8)      v_mfma_i32_32x32x32_i8, exact
-//   S[t][r]  = d_a[t][b]·d_w[r][b]                v_mfma_f32_32x32x2_f32 (rank-1)
+//   S[t][r]  = d_a[t][b]·d_w[r][b]                v_mfma_f32_32x32x1f32 (outer product;
+//                                                  two blocks' S per instruction)
 //   acc      = fma((float)I, S, acc)              VALU
 // so each block contributes (d_w·d_a)·isum exactly as the reference's block dot
 // does; only the order of the f32 sum over blocks differs.  Weights stay in
@@ -28,6 +29,7 @@ namespace rie {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 
 struct GemmP {
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][t][v] = 0.0f;
     const v16i zi = {0};
-    const v16f zf = {0};
+    const v32f zf32 = {0};
 
     // Stage ring: LDS holds stages s (being multiplied) and s + 1; two register sets
     // hold the global loads of stages s + 1 and s + 2, so a stage's loads are issued
@@ -239,23 +241,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
         if (s < n_stages) {  // workgroup-uniform; the idle step of an odd stage count skips it
             const GemmStage<TY, GLU, BN> &S = st[s & 1];
             v4i bw[G_KC][NW], av[G_KC][NT];
-            float bs[G_KC][NW], as[G_KC][NT];
 #pragma unroll
             for (int j = 0; j < G_KC; j++) {
 #pragma unroll
                 for (int a = 0; a < NW; a++) {
                     const uint4 q = *(const uint4 *)(S.wq[a] + wrow * WST + j * QB + 16 * h);
                     bw[j][a] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
-                    bs[j][a] = l < 32 ? S.dw[a][wrow * G_KC + j] : 0.0f;
                 }
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    av[j][t] = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
-                    as[j][t] = l < 32 ? S.da[arow[t] * G_KC + j] : 0.0f;
-                }
+                for (int t = 0; t < NT; t++) av[j][t] = *(const v4i *)(S.a + arow[t] * G_AST + 32 * j + 16 * h);
+            }
+            // scale operands of the product pairs (2i, 2i + 1): lane half h supplies
+            // product 2i + h's, for the two-block outer product v_mfma_f32_32x32x1f32
+            // (block h's 32×32 result in registers 16h..16h+15, laid out as a single
+            // block's); one such MFMA per two products halves the scale-MFMA cycles
+            float sa[P / 2], sb[P / 2];
+#pragma unroll
+            for (int i = 0; i < P / 2; i++) {
+                const int qh = 2 * i + h;
+                const int jh = qh / (NT * NW), th = (qh / NW) % NT, ah = qh % NW;
+                const int arh = wc * 32 * NT + 32 * th + tok_m;
+                sa[i] = S.da[arh * G_KC + jh];
+                sb[i] = S.dw[ah][wrow * G_KC + jh];
             }
             v16i Iq[2];
-            v16f Sq[2];
+            v32f Sp[2];
             // The MFMAs of product q take an (empty asm) dependency on the finished
             // accumulators of product q-2: at most two result pairs are live, and the
             // MFMAs of q overlap the VALU epilogue of q-1.
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
                                  "v"(d[8]), "v"(d[9]), "v"(d[10]), "v"(d[11]), "v"(d[12]), "v"(d[13]), "v"(d[14]), "v"(d[15]));
                 }
                 Iq[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bw[j][a], zi, 0, 0, 0);
-                Sq[q & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(as[j][t], bs[j][a], zf, 0, 0, 0);
+                if ((q & 1) == 0) Sp[(q >> 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x1f32(sa[q >> 1], sb[q >> 1], zf32, 0, 0, 0);
             };
             issue(0);
 #pragma unroll
@@ -282,7 +292,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
                 __builtin_amdgcn_sched_barrier(0);
                 const int t = (q / NW) % NT, a = q % NW;
 #pragma unroll
-                for (int v = 0; v < 16; v++) acc[a][t][v] = fmaf((float)Iq[q & 1][v], Sq[q & 1][v], acc[a][t][v]);
+                for (int v = 0; v < 16; v++)
+                    acc[a][t][v] = fmaf((float)Iq[q & 1][v], Sp[(q >> 1) & 1][16 * (q & 1) + v], acc[a][t][v]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
