@@ -38,6 +38,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef _Float16 half8k __attribute__((ext_vector_type(8)));
 
 struct KqP {
     const uint8_t *w[3];
@@ -194,6 +196,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     const int arow = wc * 32 + tok_m;  // this lane's token row of the A operands
     const v16i zi = {0};
     const v16f zf = {0};
+    const v32f zf32 = {0};
 
     float acc[NW][16];
     int s1[NW][16];
@@ -231,15 +234,28 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
         if (hs == 1) {  // end of the superblock: the min term and the two scale products
 #pragma unroll
             for (int a = 0; a < NW; a++) {
-                v16f s2 = zf;
+                // Σ_j m_j·bs_j exactly on one f16 MFMA: k-slots 2j, 2j + 1 hold the base-64
+                // digits of the block sum (bs = 64·hi + lo, |bs| ≤ 32·127) against m_j and
+                // 64·m_j; every product and partial sum is an integer below 2^24.  Lane half h
+                // supplies sub-blocks 4h..4h+3.
+                half8k ab, bb;
 #pragma unroll
-                for (int k = 0; k < 4; k++)  // Σ_j m_j·bs_j, sub-blocks 2k + h of each lane half
-                    s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(S.bs[arow * 8 + 2 * k + h], S.wm[a][wrow * 8 + 2 * k + h], s2, 0, 0, 0);
-                const v16f p1 = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? S.da[arow] : 0.0f, h == 0 ? S.wd[a][wrow] : 0.0f, zf, 0, 0, 0);
-                const v16f p2 = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? S.da[arow] : 0.0f, h == 0 ? S.wdm[a][wrow] : 0.0f, zf, 0, 0, 0);
+                for (int q = 0; q < 4; q++) {
+                    const int j = 4 * h + q;
+                    const int bsj = (int)S.bs[arow * 8 + j];
+                    const float mj = S.wm[a][wrow * 8 + j];
+                    ab[2 * q] = (_Float16)(float)(bsj & 63);
+                    ab[2 * q + 1] = (_Float16)(float)(bsj >> 6);
+                    bb[2 * q] = (_Float16)mj;
+                    bb[2 * q + 1] = (_Float16)(64.0f * mj);
+                }
+                const v16f s2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ab, bb, zf, 0, 0, 0);
+                // d·d_a and dmin·d_a in one two-block outer product (block 0: lanes 0-31, d;
+                // block 1: lanes 32-63, dmin)
+                const v32f pp = __builtin_amdgcn_mfma_f32_32x32x1f32(S.da[arow], h == 0 ? S.wd[a][wrow] : S.wdm[a][wrow], zf32, 0, 0, 0);
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    acc[a][v] += p1[v] * (float)s1[a][v] - p2[v] * s2[v];
+                    acc[a][v] += pp[v] * (float)s1[a][v] - pp[16 + v] * s2[v];
                     s1[a][v] = 0;
                 }
             }
