@@ -181,7 +181,7 @@ __device__ __forceinline__ void stage_store(GemmStage<TY, GLU, BN> &S, int tid, 
 }
 
 template <int TY, bool GLU, int NT>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmP p) {
+__global__ __launch_bounds__(256, (!GLU && NT == 1) ? 3 : 2) void gemm_kernel(GemmP p) {  // one-tile non-gated: three waves per SIMD
     constexpr int NW = GLU ? 2 : 1;
     constexpr int BN = 64 * NT;  // tokens per workgroup tile: NT 32-token tiles per wave, 2 waves along tokens
     constexpr int QB = GemmLds<TY>::QB, WST = GemmLds<TY>::WST;
