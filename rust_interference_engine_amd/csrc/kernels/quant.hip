@@ -167,12 +167,20 @@ void launch_rmsnorm(const float *x, int ldx, const float *w, float eps, int n_ro
 }
 
 // ---- token embedding: dequantize_row (quant/reference.rs:53-215) ---------------
+// Token ids from the host are checked there; an id made on the device (the greedy
+// argmax of a row without a finite maximum gives 0x7fffffff) that is not a row of
+// the table gives a NaN row instead of a read past the table.
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t *__restrict__ tokens, const uint8_t *__restrict__ table, int ty,
-                                                    int E, size_t rb, float scale, float *__restrict__ x) {
+                                                    int E, size_t rb, uint32_t n_rows, float scale, float *__restrict__ x) {
     const int t = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= E) return;
-    const uint8_t *row = table + (size_t)tokens[t] * rb;
+    const uint32_t tok = tokens[t];
+    if (tok >= n_rows) {
+        x[(size_t)t * E + i] = __builtin_nanf("");
+        return;
+    }
+    const uint8_t *row = table + (size_t)tok * rb;
     float y = 0.0f;
     switch (ty) {
     case T_F32: y = ((const float *)row)[i]; break;
@@ -290,7 +298,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t *__restrict__
 
 void launch_embed(const uint32_t *tokens, int n, const DevWeight &table, float scale, float *x, hipStream_t st) {
     const int E = (int)table.cols;
-    hipLaunchKernelGGL(embed_kernel, dim3((E + 255) / 256, n), dim3(256), 0, st, tokens, table.data, table.ty, E, table.rb(), scale, x);
+    hipLaunchKernelGGL(embed_kernel, dim3((E + 255) / 256, n), dim3(256), 0, st, tokens, table.data, table.ty, E, table.rb(),
+                       (uint32_t)table.rows, scale, x);
 }
 
 }  // namespace rie

@@ -359,13 +359,22 @@ PROLOGUE_WIDTHS = {  # hidden sizes past one superblock / one 4096-value pass, a
     None: None,
     "e2048_ff768": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 2048), ("n_ff_exp", 768), ("n_ff", 1536))],
     "e4096": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 4096), ("n_ff", 1024), ("n_ff_exp", 768))],
+    # the benchmark workloads' attention shapes: head dim 128, 4 / 8 / 2 query heads per KV head
+    "heads_32_8": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 4096), ("n_ff", 1024), ("n_head", 32),
+                                                           ("n_head_kv", 8), ("head_dim", 128), ("rope_dim", 128))],
+    "heads_32_4": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 4096), ("n_ff", 1024), ("n_head", 32),
+                                                           ("n_head_kv", 4), ("head_dim", 128), ("rope_dim", 128))],
+    "heads_16_8": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 2048), ("n_ff", 1024), ("n_head", 16),
+                                                           ("n_head_kv", 8), ("head_dim", 128), ("rope_dim", 128))],
 }
 
 
 @pytest.mark.parametrize("arch,ty,width", [("qwen3moe", Q4_K, None), ("qwen3moe", Q4_0, None), ("llama", Q4_0, None),
                                            ("llama", Q4_K, None), ("qwen3moe", Q4_K, "e2048_ff768"),
                                            ("qwen3moe", Q4_0, "e2048_ff768"), ("llama", Q4_0, "e4096"),
-                                           ("llama", Q4_K, "e4096"), ("llama", Q4_K, "e2048_ff768")])
+                                           ("llama", Q4_K, "e4096"), ("llama", Q4_K, "e2048_ff768"),
+                                           ("llama", Q4_0, "heads_32_8"), ("llama", Q4_0, "heads_32_4"),
+                                           ("llama", Q4_0, "heads_16_8")])
 def test_decode_prologues_equal_standalone_norm(oracle, cuda, arch, ty, width):
     """One-token decode normalizes x inside the GEMVs that read it: Q/K/V and
     gate/up (activation codes), and for MoE layers the router (f32 rows) and the
@@ -373,7 +382,8 @@ def test_decode_prologues_equal_standalone_norm(oracle, cuda, arch, ty, width):
     standalone RMSNorm and quantizer launches instead.  Decoding the same tokens
     at the same positions both ways gives bitwise equal logits, at hidden sizes
     from one superblock to 4096 (several superblocks and 4096-value passes per
-    workgroup) and at the 768-wide expert FFN."""
+    workgroup), at the 768-wide expert FFN and at the benchmark workloads'
+    attention shapes (head dim 128)."""
     spec, g, _ = _pair(oracle, arch, ty, 0, n_ctx=64, max_batch=16, mutate=PROLOGUE_WIDTHS[width])
     toks = [(i * 41 + 7) % spec.n_vocab for i in range(20)]
     g.forward(toks[:16], 0)
