@@ -61,7 +61,8 @@ __host__ __device__ constexpr int turbo_block(int d) {
 // xs, ys: this wave's LDS scratch, 256 floats each; s_inv: 8 floats.
 // HD > 0: the head size as a compile-time constant (HD = a.hd).
 constexpr int KV_MIRROR_SC = 512;  // byte offset of the scales in a mirror row
-template <int HD>
+// KVT ≥ 0: the cache type as a compile-time constant (KVT = a.kv_type).
+template <int HD, int KVT = -1>
 __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, int pos, float *q_dst, float *xs, float *ys,
                                float *s_inv, uint8_t *mirror = nullptr) {
     const int lane = threadIdx.x & 63;
@@ -142,14 +143,15 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
     const int slot = pos % a.slots;
     const size_t row = (size_t)h * a.slots + slot;
     uint8_t *cache = kind == 1 ? a.k_cache : a.v_cache;
-    if (a.kv_type == 0) {
+    const int kvt = KVT >= 0 ? KVT : a.kv_type;
+    if (kvt == 0) {
         uint16_t *dst = (uint16_t *)cache + row * hd;
         for (int e = lane; e < hd; e += 64) {
             const uint16_t hb = f2h(xs[e]);
             dst[e] = hb;
             if (mirror) ((uint16_t *)mirror)[e] = hb;
         }
-    } else if (a.kv_type == 1) {
+    } else if (kvt == 1) {
         // store_q8_0 (cpu.rs:637-647): round half away from zero, f16 scale
         uint8_t *dst = cache + row * (size_t)(hd / 32 * 34);
         for (int e0 = 0; e0 < hd; e0 += 64) {
@@ -200,20 +202,58 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
         uint8_t *codes = cache + row * (size_t)(hd / 2);
         uint16_t *scales = (kind == 1 ? a.k_scale : a.v_scale) + row * (size_t)(hd / b);
         uint8_t *qv = (uint8_t *)ys;  // 256 code bytes
-        const int nbk = hd / b;
-        if (lane < nbk) {  // sequential f32 sums, the reference's order
-            float ss = 0.0f;
-            for (int j = 0; j < b; j++) ss += xs[lane * b + j] * xs[lane * b + j];
-            const float rms = sqrtf(ss / (float)b);
-            s_inv[lane] = rms > 0.0f ? 1.0f / rms : 0.0f;
-        }
-        wave_sync();
-        for (int e = lane; e < hd; e += 64) {
-            const float v = xs[e] * s_inv[e / b];
-            uint8_t q = 0;
+        // The per-block sums run in the reference's order, sequential f32 adds over the
+        // block's values (turbo.rs:148-164): every lane forms its values' products at
+        // once (the same roundings as the reference's x·x and x·c), then one chain of
+        // adds, the same in every lane, reads them in element order with readlane.
+        // chain(p, fin): Σ over each block of p(e) in order e = 0, 1, …; fin(block, sum)
+        // at the end of every block.
+        float xv[4];
 #pragma unroll
-            for (int k = 0; k < 15; k++) q += (uint8_t)(v > 0.5f * (c[k] + c[k + 1]));
-            qv[e] = q;
+        for (int k = 0; k < 4; k++) xv[k] = lane + 64 * k < hd ? xs[lane + 64 * k] : 0.0f;
+        auto chain = [&](const float (&pv)[4], auto fin) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (64 * k >= hd) break;
+                const int pk = __float_as_int(pv[k]);
+#pragma unroll
+                for (int l = 0; l < 64; l++) {
+                    const int e = 64 * k + l;
+                    if (e >= hd) break;  // hd = 32: half a chunk
+                    acc = acc + __int_as_float(__builtin_amdgcn_readlane(pk, l));
+                    if (((e + 1) & (b - 1)) == 0) {
+                        fin(e / b, acc);
+                        acc = 0.0f;
+                    }
+                }
+            }
+        };
+        float sq[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) sq[k] = xv[k] * xv[k];
+        chain(sq, [&](int bk, float ss) {
+            const float rms = sqrtf(ss / (float)b);
+            if (lane == 0) s_inv[bk] = rms > 0.0f ? 1.0f / rms : 0.0f;
+        });
+        wave_sync();
+        float px[4], pc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = lane + 64 * k;
+            px[k] = pc[k] = 0.0f;
+            if (e < hd) {
+                const float v = xv[k] * s_inv[e / b];
+                int q = 0;
+#pragma unroll
+                for (int i = 0; i < 15; i++) q += v > 0.5f * (c[i] + c[i + 1]) ? 1 : 0;
+                qv[e] = (uint8_t)q;
+                float cq = c[0];
+#pragma unroll
+                for (int i = 1; i < 16; i++) cq = q == i ? c[i] : cq;
+                px[k] = xv[k] * cq;
+                pc[k] = cq * cq;
+            }
         }
         wave_sync();
         for (int i = lane; i < hd / 2; i += 64) {  // byte i holds values g (low) and g+16 (high) of its 32-chunk
@@ -221,16 +261,19 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
             codes[i] = (uint8_t)(qv[g] | (qv[g + 16] << 4));
             if (mirror) mirror[i] = (uint8_t)(qv[g] | (qv[g + 16] << 4));
         }
-        if (lane < nbk) {
-            float num = 0.0f, den = 0.0f;
-            for (int j = 0; j < b; j++) {
-                const float cq = c[qv[lane * b + j]];
-                num += xs[lane * b + j] * cq;
-                den += cq * cq;
+        // least-squares scale Σx·c / Σc² per block (the two sums of one sequential loop);
+        // the numerators wait in LDS past the codes (lane 0 writes and reads them)
+        float *nums = ys + 128;
+        chain(px, [&](int bk, float num) {
+            if (lane == 0) nums[bk] = num;
+        });
+        chain(pc, [&](int bk, float den) {
+            if (lane == 0) {
+                const uint16_t hb = f2h(den > 0.0f ? nums[bk] / den : 0.0f);
+                scales[bk] = hb;
+                if (mirror) ((uint16_t *)(mirror + KV_MIRROR_SC))[bk] = hb;
             }
-            scales[lane] = f2h(den > 0.0f ? num / den : 0.0f);
-            if (mirror) ((uint16_t *)(mirror + KV_MIRROR_SC))[lane] = f2h(den > 0.0f ? num / den : 0.0f);
-        }
+        });
     }
 }
 
@@ -503,22 +546,30 @@ __device__ __forceinline__ void query_registers(const AttnArgs &a, int G, int hd
     const int tid = threadIdx.x;
     if constexpr (KVT != 0) {
         if constexpr (KVT == 2) {
-            for (int j = 0; j < G; j++) {
-                float *x = qs_f + j * hd;
-                for (int e = tid; e < hd; e += 256) x[e] *= a.turbo_signs[e];
-                __syncthreads();
-                for (int hstep = 1; hstep < tb; hstep *= 2) {
-                    for (int k = tid; k < hd / 2; k += 256) {
-                        const int blk = k / (tb / 2), kk = k % (tb / 2);
-                        const int jj = blk * tb + (kk / hstep) * 2 * hstep + (kk % hstep);
-                        const float x0 = x[jj], x1 = x[jj + hstep];
-                        x[jj] = x0 + x1;
-                        x[jj + hstep] = x0 - x1;
+            // every head of the group at once, one barrier per butterfly stage; the
+            // signs (exact ±1 factors) are applied as the first stage reads its
+            // operands and 1/√tb as the last stage writes, the same roundings as
+            // sign pass, stages, scale pass
+            const float sq = 1.0f / sqrtf((float)tb);
+            for (int hstep = 1; hstep < tb; hstep *= 2) {
+                for (int k = tid; k < G * hd / 2; k += 256) {
+                    const int j = k / (hd / 2), kh = k % (hd / 2);
+                    const int blk = kh / (tb / 2), kk = kh % (tb / 2);
+                    const int e = blk * tb + (kk / hstep) * 2 * hstep + (kk % hstep);
+                    float *x = qs_f + j * hd;
+                    float x0 = x[e], x1 = x[e + hstep];
+                    if (hstep == 1) {
+                        x0 *= a.turbo_signs[e];
+                        x1 *= a.turbo_signs[e + hstep];
                     }
-                    __syncthreads();
+                    float y0 = x0 + x1, y1 = x0 - x1;
+                    if (2 * hstep == tb) {
+                        y0 *= sq;
+                        y1 *= sq;
+                    }
+                    x[e] = y0;
+                    x[e + hstep] = y1;
                 }
-                const float sq = 1.0f / sqrtf((float)tb);
-                for (int e = tid; e < hd; e += 256) x[e] *= sq;
                 __syncthreads();
             }
         }
@@ -900,7 +951,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     } else {
         for (int v = wv; v < nv; v += 4) {
             const int kind = v < H ? 0 : v - H + 1;
-            prep_head_wave<HD>(hp, kind, kind == 0 ? h0 + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
+            prep_head_wave<HD, KVT>(hp, kind, kind == 0 ? h0 + v : g, 0, p, qs_f + v * hd, pscr[wv], pscr[wv] + 256, pscr[wv] + 512,
                                kind == 0 ? nullptr : mirror[kind - 1]);
         }
     }
