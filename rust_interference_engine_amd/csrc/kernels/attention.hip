@@ -503,6 +503,23 @@ __device__ __forceinline__ void chunk_values(const KvChunk<KVT> &c, int d0, floa
     }
 }
 
+// The same 8 values as level·scale: the levels (Q8_0 codes, Turbo4 int8 levels) as
+// floats and the chunk's one scale (Q8_0 d, Turbo4 scale/46)
+template <int KVT>
+__device__ __forceinline__ float chunk_levels(const KvChunk<KVT> &c, int d0, float v[8]) {
+    static_assert(KVT == 1 || KVT == 2, "quantized caches");
+    uint32_t lv[2];
+    if constexpr (KVT == 1) {
+        lv[0] = c.raw.x;
+        lv[1] = c.raw.y;
+    } else {
+        turbo_levels8(c, (d0 % 32) >= 16, lv);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)(int8_t)((lv[i >> 2] >> (8 * (i & 3))) & 0xff);
+    return KVT == 1 ? h2f(c.sc) : h2f(c.sc) * (1.0f / 46.0f);
+}
+
 // Scores of ATT_NP positions × MG query heads: each lane's partial dot over its 8
 // dims, summed over the SUB lanes of the position (every lane of the group gets
 // the sum).  Q8_0 / Turbo4 caches: per-block integer dots (cpu.rs: int32 block
@@ -969,6 +986,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
 #pragma unroll
         for (int i = 0; i < 8; i++) o[j][i] = 0.0f;
     }
+    const bool softcap = a.softcap > 0.0f;
     for (int tile = r0; tile < r1; tile += TP) {
         if (tile != r0) load_tile<KVT, PP>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
         if (own && tile + TP >= r1) {
@@ -981,38 +999,68 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
         }
         float sc[ATT_NP][MG];
         tile_scores<KVT, SUB, MG>(kc, qf, qq, qdd, c, cact, d0, sc);
-        // online softmax of this slot's positions, per head
-        float pw[ATT_NP][MG];
+        if (softcap) {  // uniform
+#pragma unroll
+            for (int n = 0; n < ATT_NP; n++)
+#pragma unroll
+                for (int j = 0; j < MG; j++) sc[n][j] = softcap_f(sc[n][j], a.softcap);
+        }
+        // Online softmax of this slot's positions, per head.  The running maximum moves
+        // only when a score exceeds it by 8 (log2 units): probabilities stay ≤ 2⁸, and
+        // the rescale of the state runs only in tiles where some lane's maximum moved.
+        float mnew[MG];
+        bool grow = false;
 #pragma unroll
         for (int j = 0; j < MG; j++) {
             float mx = -INFINITY;
 #pragma unroll
             for (int n = 0; n < ATT_NP; n++) {
-                sc[n][j] = ok[n] ? softcap_f(sc[n][j], a.softcap) * LOG2E_F : -INFINITY;
+                sc[n][j] = ok[n] ? sc[n][j] * LOG2E_F : -INFINITY;
                 mx = fmaxf(mx, sc[n][j]);
             }
-            const float m_new = fmaxf(m_s[j], mx);
-            const bool any = m_new != -INFINITY;
-            const float al = any ? exp2_hw(m_s[j] - m_new) : 1.0f;
+            mnew[j] = mx > m_s[j] + 8.0f ? mx : m_s[j];
+            grow |= mnew[j] != m_s[j];
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int j = 0; j < MG; j++) {
+                const float al = mnew[j] != -INFINITY ? exp2_hw(m_s[j] - mnew[j]) : 1.0f;
+                l_s[j] = l_s[j] * al;
+                m_s[j] = mnew[j];
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[j][i] *= al;
+            }
+        }
+        float pw[ATT_NP][MG];
+#pragma unroll
+        for (int j = 0; j < MG; j++) {
+            const bool any = m_s[j] != -INFINITY;
             float sum = 0.0f;
 #pragma unroll
             for (int n = 0; n < ATT_NP; n++) {
-                pw[n][j] = any ? exp2_hw(sc[n][j] - m_new) : 0.0f;
+                pw[n][j] = any ? exp2_hw(sc[n][j] - m_s[j]) : 0.0f;
                 sum += pw[n][j];
             }
-            l_s[j] = l_s[j] * al + sum;
-            m_s[j] = m_new;
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[j][i] *= al;
+            l_s[j] = l_s[j] + sum;
         }
 #pragma unroll
         for (int n = 0; n < ATT_NP; n++) {
             float vv[8];
-            chunk_values<KVT>(vc[n], d0, vv);
+            if constexpr (KVT == 0) {
+                chunk_values<KVT>(vc[n], d0, vv);
 #pragma unroll
-            for (int j = 0; j < MG; j++)
+                for (int j = 0; j < MG; j++)
 #pragma unroll
-                for (int i = 0; i < 8; i++) o[j][i] = fmaf(pw[n][j], vv[i], o[j][i]);
+                    for (int i = 0; i < 8; i++) o[j][i] = fmaf(pw[n][j], vv[i], o[j][i]);
+            } else {  // the chunk's scale goes on the probability (axpy_rotated_4's weight)
+                const float vs = chunk_levels<KVT>(vc[n], d0, vv);
+#pragma unroll
+                for (int j = 0; j < MG; j++) {
+                    const float w = pw[n][j] * vs;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) o[j][i] = fmaf(w, vv[i], o[j][i]);
+                }
+            }
         }
     }
     // ---- merge the slots of the wave (lane groups SUB apart) ----
