@@ -160,6 +160,7 @@ __device__ __forceinline__ float wave_max(float v, int width) {
 // 2^x by the hardware exponential (v_exp_f32): exp2(-inf) = 0
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr float LOG2E_F = 1.44269504088896340736f;
+constexpr float LN2_F = 0.69314718055994530942f;
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -109,6 +109,9 @@ bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream
 // partials); false when the shape or cache type is not covered.
 bool attention_prompt_mfma_ok(const AttnArgs &a);
 bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st);
+// Merge of a.n_split range partials per (token, head) [t][head][split][hd + 2]
+// (maximum in natural-log units), the inverse Turbo4 rotation, f32 att and Q8_0.
+void launch_attention_combine(const AttnArgs &a, hipStream_t st);
 // number of context ranges (n_split) for a launch whose longest query sees max_len positions
 constexpr int ATT_MAX_SPLIT = 256;
 int attention_splits(int n_tok, int n_kv, int max_len);

@@ -1324,6 +1324,10 @@ void launch_attention(const AttnArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_head, a.n_tok), dim3(256), 0, st, a);
 }
 
+void launch_attention_combine(const AttnArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_head, a.n_tok), dim3(256), 0, st, a);
+}
+
 bool attention_fused_ok(const AttnArgs &a) {
     const int G = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
     // the range merge reads whole batches of 16 ranges past the first: n_split a power of two

@@ -31,6 +31,7 @@
 #include "../device.hpp"
 #include "../kernels.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace rie {
@@ -131,13 +132,16 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
     const int pos_t = pos0 + t;
     const int start_t = a.window > 0 ? max(0, pos_t + 1 - a.window) : 0;
 
-    // workgroup position range
+    // workgroup position range, and of it the tiles [t_lo, t_hi) of KV split blockIdx.z
     const int t_first = tr * tbw * 32;
     const int t_last = min(a.n_tok, (tr + 1) * tbw * 32) - 1;
     const int p_hi = pos0 + t_last;
     const int p_lo = a.window > 0 ? max(0, pos0 + t_first + 1 - a.window) : 0;
     const int k0 = p_lo & ~(PT - 1);
-    const int n_tiles = (p_hi - k0) / PT + 1;
+    const int n_all = (p_hi - k0) / PT + 1;
+    const int per = (n_all + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int t_lo = min(n_all, (int)blockIdx.z * per), t_hi = min(n_all, t_lo + per);
+    const int n_tiles = t_hi;
     // wave-uniform bounds of its tokens' visible positions
     const int w_tmin = tb * 32, w_tmax = min(a.n_tok, tb * 32 + 32) - 1;
     const int w_pmax = pos0 + w_tmax;
@@ -262,21 +266,22 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; v++) o[d][v] = 0.0f;
 
-    // group tile i is T(i) = grp + i·NW; buffer i & 1 holds T(i) during iteration i, and
-    // the register sets hold T(i+1) and T(i+2) (issued two iterations before their use)
-    const int n_iter = (n_tiles + NW - 1) / NW;
+    // group tile i is T(i) = t_lo + grp + i·NW; buffer i & 1 holds T(i) during iteration
+    // i, and the register sets hold T(i+1) and T(i+2) (issued two iterations before
+    // their use)
+    const int n_iter = (t_hi - t_lo + NW - 1) / NW;
     // Loads are issued unconditionally (tile indices past the end repeat the last
-    // tile) so that every wait for a register set is an exact count of the loads
-    // issued after it.
+    // tile; an empty split loads tile 0) so that every wait for a register set is an
+    // exact count of the loads issued after it.
     Regs ra, rb;
-    const int last = n_tiles - 1;
-    fetch(min(grp, last), ra);
+    const int last = max(n_tiles - 1, 0);
+    fetch(min(t_lo + grp, last), ra);
     stage(ra, 0);
-    fetch(min(grp + NW, last), rb);
-    fetch(min(grp + 2 * NW, last), ra);
+    fetch(min(t_lo + grp + NW, last), rb);
+    fetch(min(t_lo + grp + 2 * NW, last), ra);
     __syncthreads();
     auto body = [&](int it, Regs &x) {
-        const int tile = grp + it * NW;
+        const int tile = t_lo + grp + it * NW;
         stage(x, (it + 1) & 1);
         fetch(min(tile + 3 * NW, last), x);
         k_s = tiles + (it & 1) * TB;
@@ -396,6 +401,7 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
             L += (M == -INFINITY || mq == -INFINITY) ? 0.0f : ls[q * 256 + tid] * exp2_hw(mq - M);
         }
         l_half = L;
+        m = M;  // o and l are relative to the merged maximum from here on
 #pragma unroll
         for (int d = 0; d < DT; d++) {
             if (grp > 0)
@@ -417,6 +423,28 @@ __global__ __launch_bounds__(256 * NW) void attn_prompt_f16_kernel(AttnArgs a) {
     }
     if (!wave_on) return;
     const float l_tot = l_half + xor_f<32>(l_half);
+    if (gridDim.z > 1) {
+        // KV split: this range's partial (unnormalized output, maximum in natural-log
+        // units, sum) in the layout attn_combine_kernel merges: [t][head][split][hd + 2]
+        if (tok_ok) {
+            float *pp = a.part + (((size_t)t * a.n_head + head) * gridDim.z + blockIdx.z) * (hd + 2);
+            const float osc = KVT == 2 ? 1.0f / 256.0f : 1.0f;
+#pragma unroll
+            for (int d = 0; d < DT; d++)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    f32x4 w4;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w4[e] = o[d][4 * q4 + e] * osc;
+                    *(f32x4 *)(pp + 32 * d + 8 * q4 + 4 * h) = w4;
+                }
+            if (h == 0) {
+                pp[hd] = m == -INFINITY ? -INFINITY : m * LN2_F;
+                pp[hd + 1] = l_tot;
+            }
+        }
+        return;
+    }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     // lane: token col, dims 32d + 8(v/4) + 4h + v%4
     if constexpr (KVT == 2) {
@@ -589,25 +617,42 @@ bool attention_prompt_mfma_ok(const AttnArgs &a) {
            G <= 8 && a.n_head == G * a.n_kv && (a.att_fmt != ACT_Q8_0 || (a.att_q.qs && a.att_q.d));
 }
 
+// KV splits of a launch: long rows are split over grid.z workgroups (at least 16
+// tiles of 32 positions each, up to about two workgroups per CU, at most 16) whose
+// partials attn_combine_kernel merges.  Rows under 1024 positions keep one pass:
+// at a 512-token prompt from position 0, two splits (8 tiles each) and the merge
+// launch measured 29.3 k tok/s against 31.1 k.
+static int prompt_kv_splits(const AttnArgs &a, const dim3 &grid) {
+    const int longest = (a.pos0 + a.n_tok - 1) / PT + 1;  // tiles of the last query row (no window)
+    const int by_work = longest / 16, by_grid = 512 / (int)(grid.x * grid.y);
+    return std::max(1, std::min(16, std::min(by_work, by_grid)));
+}
+
 bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st) {
     if (!attention_prompt_mfma_ok(a)) return false;
     const int G = a.n_head / a.n_kv;
     const int wpt = G < 4 ? G : 4, tbw = 4 / wpt, hgroups = (G + 3) / 4;
-    const dim3 grid((a.n_tok + 32 * tbw - 1) / (32 * tbw), a.n_kv * hgroups);
+    dim3 grid((a.n_tok + 32 * tbw - 1) / (32 * tbw), a.n_kv * hgroups);
+    const int S = a.window > 0 ? 1 : prompt_kv_splits(a, grid);
+    grid.z = S;
+    AttnArgs b = a;
+    b.n_split = S;
+    // partials [t][head][split][hd + 2] at the start of the range-partial buffer; the
+    // Turbo4 path's rotated, quantized queries after them
+    float *qhat = a.part + (S > 1 ? (size_t)a.n_tok * a.n_head * S * (a.hd + 2) : 0);
     if (a.kv_type == 2) {
-        // the rotated, quantized queries go to the range-partial buffer (unused on this path)
-        hipLaunchKernelGGL(turbo_query_kernel, dim3(a.n_head, a.n_tok), dim3(64), 0, st, a.q, a.n_head * 128, a.turbo_signs, a.part);
-        AttnArgs b = a;
-        b.q = a.part;
+        hipLaunchKernelGGL(turbo_query_kernel, dim3(a.n_head, a.n_tok), dim3(64), 0, st, a.q, a.n_head * 128, a.turbo_signs, qhat);
+        b.q = qhat;
         launch_nw<128, 2, 2>(b, grid, st);
-        return true;
+    } else {
+        switch (a.hd) {
+        case 32: launch_nw<32, 2, 0>(b, grid, st); break;
+        case 64: launch_nw<64, 2, 0>(b, grid, st); break;
+        case 96: launch_nw<96, 2, 0>(b, grid, st); break;
+        default: launch_nw<128, 2, 0>(b, grid, st); break;
+        }
     }
-    switch (a.hd) {
-    case 32: launch_nw<32, 2, 0>(a, grid, st); break;
-    case 64: launch_nw<64, 2, 0>(a, grid, st); break;
-    case 96: launch_nw<96, 2, 0>(a, grid, st); break;
-    default: launch_nw<128, 2, 0>(a, grid, st); break;
-    }
+    if (S > 1) launch_attention_combine(b, st);
     return true;
 }
 

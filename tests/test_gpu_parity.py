@@ -539,6 +539,67 @@ def test_turbo_prompt_attention_matches_f64_on_captured_rows(oracle, cuda, nh, n
                         f"G {G} layer {layer} token {p} head {hq}: {err}"
 
 
+@pytest.mark.parametrize("kv", [0, 2])
+def test_prompt_attention_kv_splits_match_f64(oracle, cuda, kv):
+    """Prompt batches far into the context split each query block's positions over
+    several workgroups (2 at positions 1024.., 8 at 4032..), whose partials the range
+    merge combines (and, for Turbo4, rotates back); a batch at 256.. stays in one
+    pass.  Outputs against float64 on the captured queries and cache rows, to the
+    bounds of the single-pass tests."""
+    hd, nh, nkv = 128, 8, 2
+
+    def mut(s):
+        s.head_dim, s.n_head, s.n_head_kv, s.rope_dim = hd, nh, nkv, hd
+    n_ctx = 4096
+    spec, g, _ = _pair(oracle, "llama", Q8_0, kv, n_ctx=n_ctx, max_batch=64, mutate=mut)
+    G, qd = nh // nkv, nh * hd
+    toks = [(i * 53 + 11) % spec.n_vocab for i in range(n_ctx)]
+    checked = 0
+    for pos0 in range(0, n_ctx, 64):
+        n = 64
+        check = pos0 in (256, 1024, 4032)
+        g.set_capture(check)
+        g.forward(toks[pos0:pos0 + n], pos0)
+        if not check:
+            continue
+        for layer in range(spec.n_layer):
+            q = g.capture(layer, 3, n * qd).reshape(n, nh, hd)
+            att = g.capture(layer, 2, n * qd).reshape(n, nh, hd)
+            kr, ksc = g.kv_layer(layer, 0, nkv, n_ctx)
+            vr, vsc = g.kv_layer(layer, 1, nkv, n_ctx)
+            if kv == 0:
+                K = kr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+                V = vr.view(np.float16).reshape(nkv, n_ctx, hd).astype(np.float64)
+            else:
+                # largest decoded V value up to each position in either domain; the
+                # rotation is orthogonal, so a row's 2-norm bounds its unrotated values
+                vrun = []
+                for h in range(nkv):
+                    _, _, vv = _turbo_attention_f64(oracle, q[0, 0], kr[h, :pos0 + n], ksc[h, :pos0 + n], vr[h, :pos0 + n],
+                                                    vsc[h, :pos0 + n], hd)
+                    m = np.maximum(np.abs(vv).max(axis=1), np.sqrt((vv * vv).sum(axis=1)))
+                    vrun.append(np.maximum.accumulate(m))
+            for t in range(0, n, 3 if kv == 0 else 7):
+                p = pos0 + t
+                for hq in range(nh):
+                    h = hq // G
+                    if kv == 0:
+                        sc = K[h, :p + 1] @ q[t, hq].astype(np.float64)
+                        w = np.exp(sc - sc.max())
+                        ref = (w / w.sum()) @ V[h, :p + 1]
+                        vmax = np.max(np.abs(V[h, :p + 1]))
+                        bound = (8 * 2.0 ** -24 * np.max(np.abs(sc)) + 5e-6) * vmax + 1e-6
+                    else:
+                        ref, sc, _ = _turbo_attention_f64(oracle, q[t, hq], kr[h, :p + 1], ksc[h, :p + 1], vr[h, :p + 1],
+                                                          vsc[h, :p + 1], hd)
+                        vmax = vrun[h][p]
+                        bound = (8 * 2.0 ** -24 * np.max(np.abs(sc)) + 5e-6) * vmax + 2e-6 * vmax + 1e-6
+                    err = np.max(np.abs(att[t, hq] - ref))
+                    assert err <= bound, f"kv{kv} layer {layer} token {p} head {hq}: {err} > {bound}"
+                    checked += 1
+    assert checked > 0
+
+
 @pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
 def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv):
     """Single-token attention (the fused launch: prep, append, context ranges,
