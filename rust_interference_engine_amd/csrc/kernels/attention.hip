@@ -183,6 +183,7 @@ __device__ void prep_head_wave(const HeadPrepArgs &a, int kind, int h, int t, in
         for (int e = lane; e < hd; e += 64) xs[e] *= a.turbo_signs[e];
         wave_sync();
         const int b = turbo_block(hd);
+#pragma unroll
         for (int hstep = 1; hstep < b; hstep *= 2) {
             for (int k = lane; k < hd / 2; k += 64) {
                 const int blk = k / (b / 2), kk = k % (b / 2);
@@ -408,7 +409,10 @@ __device__ void prep_finish_fast(const HeadPrepArgs &a, int kind, int h, int pos
     }
 }
 
-// one wavefront per (head vector, token); the query is rewritten in place
+// one wavefront per (head vector, token); the query is rewritten in place.
+// HD, KVT > 0 / ≥ 0: head size and cache type as compile-time constants (the
+// Turbo4 rotation's butterfly indices then cost no integer divisions)
+template <int HD, int KVT>
 __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
     const int t = blockIdx.y;
     const int hh = blockIdx.x;
@@ -424,11 +428,26 @@ __global__ __launch_bounds__(64) void head_prep_kernel(HeadPrepArgs a) {
     } else {
         kind = 2; h = hh - a.n_head - a.n_kv;
     }
-    prep_head_wave<0>(a, kind, h, t, pos0 + t, a.q + (size_t)t * a.n_head * a.hd + h * a.hd, xs, ys, s_inv);
+    prep_head_wave<HD, KVT>(a, kind, h, t, pos0 + t, a.q + (size_t)t * a.n_head * a.hd + h * a.hd, xs, ys, s_inv);
+}
+
+template <int HD>
+static void launch_head_prep_hd(const HeadPrepArgs &a, dim3 grid, hipStream_t st) {
+    switch (a.kv_type) {
+    case 0: hipLaunchKernelGGL((head_prep_kernel<HD, 0>), grid, dim3(64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((head_prep_kernel<HD, 1>), grid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((head_prep_kernel<HD, 2>), grid, dim3(64), 0, st, a); break;
+    }
 }
 
 void launch_head_prep(const HeadPrepArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(head_prep_kernel, dim3(a.n_head + 2 * a.n_kv, a.n_tok), dim3(64), 0, st, a);
+    const dim3 grid(a.n_head + 2 * a.n_kv, a.n_tok);
+    switch (a.hd) {
+    case 64: launch_head_prep_hd<64>(a, grid, st); break;
+    case 128: launch_head_prep_hd<128>(a, grid, st); break;
+    case 256: launch_head_prep_hd<256>(a, grid, st); break;
+    default: hipLaunchKernelGGL((head_prep_kernel<0, -1>), grid, dim3(64), 0, st, a); break;
+    }
 }
 
 // ---- attention over the cache ---------------------------------------------------
