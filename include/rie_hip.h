@@ -139,6 +139,11 @@ int32_t rie_hip_quantize(int32_t ty, const float *x, size_t n, uint8_t *out);
  * what = 0 x after attention, 1 x after FFN, 2 attention output, 3 q after
  * RoPE/scale, 4 k after norm/RoPE, 5 v, 6 FFN gated hidden, 7 MoE router logits. */
 int32_t rie_hip_set_capture(rie_hip_backend *b, int32_t on);
+/* on = 1: single-token attention always splits the context into ranges merged
+ * across workgroups, also at the short contexts where it otherwise runs one
+ * workgroup per query head over the whole cache (so tests can check both kernels
+ * on the same positions); on = 0: automatic (the default). */
+int32_t rie_hip_set_attention_ranges(rie_hip_backend *b, int32_t on);
 int32_t rie_hip_capture(rie_hip_backend *b, size_t layer, int32_t what, float *out, size_t len);
 /* Raw KV cache of one layer: which 0 = K, 1 = V; [kv_head][slot][row bytes];
  * Turbo4 scales ([kv_head][slot] f16) go to scales_out. */

@@ -65,6 +65,7 @@ def lib():
         "rie_hip_free": (None, [P]),
         "rie_hip_quantize": (I, [I, P, S, P]),
         "rie_hip_set_capture": (I, [P, I]),
+        "rie_hip_set_attention_ranges": (I, [P, I]),
         "rie_hip_capture": (I, [P, S, I, P, S]),
         "rie_hip_kv_layer": (I, [P, S, I, P, S, P, S]),
         "rie_hip_profile_decode": (I, [P, S, I, CP, S, P, P, S, C.POINTER(S)]),

@@ -157,6 +157,11 @@ class HipBackend:
     def set_capture(self, on: bool) -> None:
         _lib.lib().rie_hip_set_capture(self._h, int(on))
 
+    def set_attention_ranges(self, on: bool) -> None:
+        """Single-token attention over context ranges at every length (the kernel
+        used past the short-context limit); off: automatic."""
+        _lib.lib().rie_hip_set_attention_ranges(self._h, int(on))
+
     def capture(self, layer: int, what: int, n: int) -> np.ndarray | None:
         out = np.zeros(n, np.float32)
         rc = _lib.lib().rie_hip_capture(self._h, layer, what, out.ctypes.data, n)

@@ -861,7 +861,16 @@ void HipBackend::greedy_step_graph(size_t pos) {
 }
 
 int HipBackend::splits_for(size_t n, size_t pos) const {
-    return attention_splits((int)n, (int)m_.cfg.n_head_kv, (int)(pos + n));
+    const ModelConfig &c = m_.cfg;
+    AttnArgs probe{};  // the shape fields attention_fused_ok looks at
+    probe.n_tok = (int)n;
+    probe.n_head = (int)c.n_head;
+    probe.n_kv = (int)c.n_head_kv;
+    probe.hd = (int)c.head_dim;
+    probe.counters = d_attn_cnt_;
+    probe.n_split = 1;
+    return attention_splits((int)n, (int)c.n_head_kv, (int)(pos + n), (int)c.head_dim,
+                            attention_fused_ok(probe) && !attn_ranges_only_);
 }
 
 const float *HipBackend::hidden(size_t *rows) {

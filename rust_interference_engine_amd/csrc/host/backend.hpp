@@ -50,6 +50,7 @@ class HipBackend {
 
     // debugging / parity hooks
     void set_capture(bool on);
+    void set_attention_ranges(bool on) { attn_ranges_only_ = on; }  // single token: range kernel at every context length
     bool capture(size_t layer, int what, float *out, size_t len);
     void kv_layer(size_t layer, int which, uint8_t *out, size_t len, uint8_t *scales_out, size_t scales_len);
     size_t kv_row_bytes() const;
@@ -149,6 +150,7 @@ class HipBackend {
     bool head_normed_ = true;   // d_xn_ holds the head's normalized rows (else Backend::hidden forms them)
     std::vector<float> hidden_host_;
     bool capture_ = false;
+    bool attn_ranges_only_ = false;
     std::vector<std::vector<std::vector<float>>> cap_;  // [what][layer]
     size_t cur_layer_ = 0;                               // layer run_layers is in (capture bookkeeping)
 

@@ -188,6 +188,10 @@ int32_t rie_hip_set_capture(rie_hip_backend *b, int32_t on) {
     return guarded(nullptr, 0, [&] { b->b->set_capture(on != 0); });
 }
 
+int32_t rie_hip_set_attention_ranges(rie_hip_backend *b, int32_t on) {
+    return guarded(nullptr, 0, [&] { b->b->set_attention_ranges(on != 0); });
+}
+
 int32_t rie_hip_capture(rie_hip_backend *b, size_t layer, int32_t what, float *out, size_t len) {
     return guarded(nullptr, 0, [&] {
         if (!b->b->capture(layer, what, out, len)) throw Error{rie::E_RUNTIME, "nothing captured"};

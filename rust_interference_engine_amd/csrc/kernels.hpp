@@ -112,9 +112,11 @@ bool launch_attention_prompt_mfma(const AttnArgs &a, hipStream_t st);
 // Merge of a.n_split range partials per (token, head) [t][head][split][hd + 2]
 // (maximum in natural-log units), the inverse Turbo4 rotation, f32 att and Q8_0.
 void launch_attention_combine(const AttnArgs &a, hipStream_t st);
-// number of context ranges (n_split) for a launch whose longest query sees max_len positions
+// number of context ranges (n_split) for a launch whose longest query sees max_len
+// positions; fused: a single token on the one-launch path (attention_fused_ok), which
+// takes one range (one workgroup per query head) at short contexts
 constexpr int ATT_MAX_SPLIT = 256;
-int attention_splits(int n_tok, int n_kv, int max_len);
+int attention_splits(int n_tok, int n_kv, int max_len, int hd, bool fused);
 
 // ---- misc.hip ----
 void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st);

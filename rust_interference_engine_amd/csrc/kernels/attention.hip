@@ -543,11 +543,11 @@ __device__ __forceinline__ float chunk_levels(const KvChunk<KVT> &c, int d0, flo
 // dims, summed over the SUB lanes of the position (every lane of the group gets
 // the sum).  Q8_0 / Turbo4 caches: per-block integer dots (cpu.rs: int32 block
 // sums) over the 4 lanes of a block, scaled by d_k·d_q.
-template <int KVT, int SUB, int MG>
-__device__ __forceinline__ void tile_scores(const KvChunk<KVT> (&kc)[ATT_NP], const float (&qf)[MG][8], const uint32_t (&qq)[MG][2],
-                                            const float (&qdd)[MG], int c, bool cact, int d0, float (&sc)[ATT_NP][MG]) {
+template <int KVT, int SUB, int MG, int NP = ATT_NP>
+__device__ __forceinline__ void tile_scores(const KvChunk<KVT> (&kc)[NP], const float (&qf)[MG][8], const uint32_t (&qq)[MG][2],
+                                            const float (&qdd)[MG], int c, bool cact, int d0, float (&sc)[NP][MG]) {
 #pragma unroll
-    for (int n = 0; n < ATT_NP; n++) {
+    for (int n = 0; n < NP; n++) {
         float kf[8];
         if constexpr (KVT == 0) chunk_values<0>(kc[n], d0, kf);
 #pragma unroll
@@ -642,12 +642,12 @@ __device__ __forceinline__ void query_registers(const AttnArgs &a, int G, int hd
     }
 }
 
-// K and V chunks of ATT_NP positions tile + pi + PP·n (rows past r1 repeat row r0)
-template <int KVT, int PP>
+// K and V chunks of NP positions tile + pi + PP·n (rows past r1 repeat row r0)
+template <int KVT, int PP, int NP = ATT_NP>
 __device__ __forceinline__ void load_tile(const AttnArgs &a, size_t kv_row0, int tile, int pi, int r0, int r1, int hd, int d0, int tb,
-                                          KvChunk<KVT> (&kc)[ATT_NP], KvChunk<KVT> (&vc)[ATT_NP], bool (&ok)[ATT_NP]) {
+                                          KvChunk<KVT> (&kc)[NP], KvChunk<KVT> (&vc)[NP], bool (&ok)[NP]) {
 #pragma unroll
-    for (int n = 0; n < ATT_NP; n++) {
+    for (int n = 0; n < NP; n++) {
         const int pos = tile + pi + PP * n;
         ok[n] = pos < r1;
         const int q = ok[n] ? pos : r0;
@@ -801,6 +801,60 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // waves.  The last workgroup of each head slice to finish merges the ranges, undoes
 // the Turbo4 rotation and writes att (f32 and Q8_0).
 
+// The G merged, normalized query heads h0 .. h0 + G - 1 in o_s (LDS) → the inverse
+// Turbo4 rotation, att (f32) and its Q8_0 codes; NT threads (every thread calls it).
+template <int HD, int G, int NT>
+__device__ void att_finish(const AttnArgs &a, int h0, float *o_s) {
+    const int tid = threadIdx.x;
+    constexpr int hd = HD;
+    if (a.kv_type == 2) {  // o ← Rᵀ o per head: block FWHT, then signs (turbo.rs:114-117)
+        const int b = turbo_block(hd);
+        for (int hstep = 1; hstep < b; hstep *= 2) {
+            for (int k = tid; k < G * hd / 2; k += NT) {
+                const int j = k / (hd / 2), kh = k % (hd / 2);
+                const int blk = kh / (b / 2), kk = kh % (b / 2);
+                const int e = j * hd + blk * b + (kk / hstep) * 2 * hstep + (kk % hstep);
+                const float x0 = o_s[e], x1 = o_s[e + hstep];
+                o_s[e] = x0 + x1;
+                o_s[e + hstep] = x0 - x1;
+            }
+            __syncthreads();
+        }
+        const float sq = 1.0f / sqrtf((float)b);
+        for (int i = tid; i < G * hd; i += NT) o_s[i] = o_s[i] * sq * a.turbo_signs[i % hd];
+        __syncthreads();
+    }
+    const size_t base = (size_t)h0 * hd;
+    for (int i = tid; i < G * hd; i += NT) a.att[base + i] = o_s[i];
+    if (a.att_fmt == ACT_Q8_0) {  // hd % 32 == 0: the group's values are whole blocks
+        // 16 lanes per block, values j and j + 16 in lane j (max and integer sums
+        // are exact in any order, so the codes are those of the reference's quantizer)
+        const int hb = tid >> 4, j = tid & 15;
+        for (int bi = hb; bi < G * hd / 32; bi += NT / 16) {
+            const float y0 = o_s[bi * 32 + j], y1 = o_s[bi * 32 + j + 16];
+            float amax = fmaxf(fabsf(y0), fabsf(y1));
+            amax = xmax_f<16>(amax);
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int q0 = (int)rintf(y0 * id), q1 = (int)rintf(y1 * id);
+            const int c0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+            const int c1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+            int su = q0 + q1, scl = c0 + c1;
+            su = xsum_i<16>(su);
+            scl = xsum_i<16>(scl);
+            const size_t e = base + bi * 32 + j;
+            a.att_q.qs[e] = (int8_t)c0;
+            a.att_q.qs[e + 16] = (int8_t)c1;
+            if (j == 0) {
+                const size_t blk = e / 32;
+                a.att_q.d[blk] = d;
+                if (a.att_q.s) a.att_q.s[blk] = d * (float)su;
+                if (a.att_q.isum) a.att_q.isum[blk] = scl;
+            }
+        }
+    }
+}
+
 // Merge of the n_split range partials of query heads h0 .. h0 + G - 1 by the last
 // workgroup (256 threads).
 // The single-token path keeps scores and running maxima in log2 units (scores
@@ -873,52 +927,7 @@ __device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts,
         if (tid + 256 * r < n_out) o_s[i] = acc * (1.0f / Ls[j]);
     }
     __syncthreads();
-    if (a.kv_type == 2) {  // o ← Rᵀ o per head: block FWHT, then signs (turbo.rs:114-117)
-        const int b = turbo_block(hd);
-        for (int hstep = 1; hstep < b; hstep *= 2) {
-            for (int k = tid; k < G * hd / 2; k += 256) {
-                const int j = k / (hd / 2), kh = k % (hd / 2);
-                const int blk = kh / (b / 2), kk = kh % (b / 2);
-                const int e = j * hd + blk * b + (kk / hstep) * 2 * hstep + (kk % hstep);
-                const float x0 = o_s[e], x1 = o_s[e + hstep];
-                o_s[e] = x0 + x1;
-                o_s[e + hstep] = x0 - x1;
-            }
-            __syncthreads();
-        }
-        const float sq = 1.0f / sqrtf((float)b);
-        for (int i = tid; i < G * hd; i += 256) o_s[i] = o_s[i] * sq * a.turbo_signs[i % hd];
-        __syncthreads();
-    }
-    const size_t base = (size_t)h0 * hd;
-    for (int i = tid; i < G * hd; i += 256) a.att[base + i] = o_s[i];
-    if (a.att_fmt == ACT_Q8_0) {  // hd % 32 == 0: the group's values are whole blocks
-        // 16 lanes per block, values j and j + 16 in lane j (max and integer sums
-        // are exact in any order, so the codes are those of the reference's quantizer)
-        const int hb = tid >> 4, j = tid & 15;
-        for (int bi = hb; bi < G * hd / 32; bi += 16) {
-            const float y0 = o_s[bi * 32 + j], y1 = o_s[bi * 32 + j + 16];
-            float amax = fmaxf(fabsf(y0), fabsf(y1));
-            amax = xmax_f<16>(amax);
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            const int q0 = (int)rintf(y0 * id), q1 = (int)rintf(y1 * id);
-            const int c0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
-            const int c1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
-            int su = q0 + q1, scl = c0 + c1;
-            su = xsum_i<16>(su);
-            scl = xsum_i<16>(scl);
-            const size_t e = base + bi * 32 + j;
-            a.att_q.qs[e] = (int8_t)c0;
-            a.att_q.qs[e + 16] = (int8_t)c1;
-            if (j == 0) {
-                const size_t blk = e / 32;
-                a.att_q.d[blk] = d;
-                if (a.att_q.s) a.att_q.s[blk] = d * (float)su;
-                if (a.att_q.isum) a.att_q.isum[blk] = scl;
-            }
-        }
-    }
+    att_finish<HD, G, 256>(a, h0, o_s);
 }
 
 
@@ -1172,6 +1181,191 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     combine_group<HD, H>(a, h0, qs_f, wo_s[0], wm_s[0]);
 }
 
+// Short contexts (attention_splits returns one range): one workgroup of ATT_HEAD_NT
+// threads per query head reads every position of its KV head, so there are no range
+// partials and no cross-workgroup arrival count (at a few hundred positions the
+// range form's chain of partial stores, release, acquire and reloads costs as much as
+// the pass over the cache).  The query heads of a group read the same K/V rows:
+// blockIdx.x = j · n_kv + g, so with 8 KV heads the heads of group g share one XCD
+// (workgroups are placed on the 8 XCDs round-robin by index) and the repeated reads
+// hit its L2; placement affects speed only.  Every workgroup's range holds the new
+// position, so each prepares, encodes and appends its K and V row (the workgroups of
+// a group write identical bytes) and reads its own LDS copy of it.  Each SUB-lane
+// position slot keeps its own online softmax state in registers; the slots are
+// merged by lane swaps within a wave and through LDS across the waves.
+constexpr int ATT_HEAD_NT = 1024;
+constexpr int ATT_HEAD_NP = 8;  // positions per slot per tile
+template <int KVT, int HD>
+__global__ __launch_bounds__(ATT_HEAD_NT) void attn_decode_head_kernel(AttnArgs a, HeadPrepArgs hp) {
+    constexpr int NT = ATT_HEAD_NT, NW = NT / 64;
+    constexpr int SUB = HD / 8;   // lanes per cache row (8 dims each)
+    constexpr int PP = NT / SUB;  // position slots
+    constexpr int NP = ATT_HEAD_NP;
+    constexpr int TP = PP * NP;   // positions per tile
+    constexpr int hd = HD;
+    constexpr int tb = turbo_block(HD);
+    const int G = a.n_head / a.n_kv;
+    const int g = blockIdx.x % a.n_kv, h = g * G + blockIdx.x / a.n_kv;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int p = a.d_pos0 ? *a.d_pos0 : a.pos0;
+    const int r0 = a.window > 0 ? max(0, p + 1 - a.window) : 0;
+    const int r1 = p + 1;
+    const int pi = tid / SUB, c = tid % SUB;
+    const int d0 = 8 * c;
+
+    __shared__ float qs_f[HD];
+    __shared__ __align__(16) int8_t qs_i[HD];
+    __shared__ float qs_d[HD / 32];
+    __shared__ __align__(16) uint8_t mirror[2][KV_MIRROR_SC + 16];  // the new position's encoded K and V rows
+    __shared__ float pscr[3][520];                                   // prep scratch of waves 0-2
+    __shared__ float wo_s[NW][HD];                                   // per-wave merged slot states
+    __shared__ float wm_s[NW], wl_s[NW];
+    __shared__ float o_s[HD];
+
+    const size_t kv_row0 = (size_t)g * a.slots;
+    KvChunk<KVT> kc[NP], vc[NP];
+    bool ok[NP];
+    // Preparation items: 0 the query head, 1 and 2 the new position's K and V, one per
+    // wave of waves 0-2.  On the register path every wave issues an item's loads (the
+    // waves past 2 item 2's, unused), so every wave has the same loads in flight ahead
+    // of its tile, and the arithmetic runs while the tile is in flight.
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
+    const int item = min(wvu, 2);
+    const bool fast = prep_fast_ok(hp, hd);
+    PrepIn<HD> pin;
+    if (fast) prep_load_fast<HD>(hp, item, item == 0 ? h : g, p, pin);
+    load_tile<KVT, PP, NP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // every row index is in range (mod slots)
+    if (wvu < 3) {
+        if (fast)
+            prep_finish_fast<HD>(hp, item, item == 0 ? h : g, p, pin, qs_f, item == 0 ? nullptr : mirror[item - 1]);
+        else
+            prep_head_wave<HD, KVT>(hp, item, item == 0 ? h : g, 0, p, qs_f, pscr[item], pscr[item] + 256, pscr[item] + 512,
+                                    item == 0 ? nullptr : mirror[item - 1]);
+    }
+    __syncthreads();
+    float qf[1][8];
+    uint32_t qq[1][2];
+    float qdd[1];
+    query_registers<KVT, 1>(a, 1, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
+
+    float m_s = -INFINITY, l_s = 0.0f, o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = 0.0f;
+    const bool softcap = a.softcap > 0.0f;
+    for (int tile = r0; tile < r1; tile += TP) {
+        if (tile != r0) load_tile<KVT, PP, NP>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
+        if (tile + TP >= r1) {
+#pragma unroll
+            for (int n = 0; n < NP; n++)
+                if (tile + pi + PP * n == p) {
+                    load_chunk<KVT>(mirror[0], (const uint16_t *)(mirror[0] + KV_MIRROR_SC), 0, hd, d0, tb, kc[n]);
+                    load_chunk<KVT>(mirror[1], (const uint16_t *)(mirror[1] + KV_MIRROR_SC), 0, hd, d0, tb, vc[n]);
+                }
+        }
+        float sc[NP][1];
+        tile_scores<KVT, SUB, 1, NP>(kc, qf, qq, qdd, c, true, d0, sc);
+        if (softcap) {  // uniform
+#pragma unroll
+            for (int n = 0; n < NP; n++) sc[n][0] = softcap_f(sc[n][0], a.softcap);
+        }
+        // online softmax of this slot's positions (log2 units); the running maximum
+        // moves only when a score exceeds it by 8, and the state is rescaled only in
+        // tiles where some lane's maximum moved
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < NP; n++) {
+            sc[n][0] = ok[n] ? sc[n][0] * LOG2E_F : -INFINITY;
+            mx = fmaxf(mx, sc[n][0]);
+        }
+        const float mnew = mx > m_s + 8.0f ? mx : m_s;
+        if (__builtin_amdgcn_ballot_w64(mnew != m_s)) {
+            const float al = mnew != -INFINITY ? exp2_hw(m_s - mnew) : 1.0f;
+            l_s = l_s * al;
+            m_s = mnew;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] *= al;
+        }
+        float pw[NP];
+        {
+            const bool any = m_s != -INFINITY;
+            float sum = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NP; n++) {
+                pw[n] = any ? exp2_hw(sc[n][0] - m_s) : 0.0f;
+                sum += pw[n];
+            }
+            l_s = l_s + sum;
+        }
+#pragma unroll
+        for (int n = 0; n < NP; n++) {
+            float vv[8];
+            if constexpr (KVT == 0) {
+                chunk_values<KVT>(vc[n], d0, vv);
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] = fmaf(pw[n], vv[i], o[i]);
+            } else {  // the chunk's scale goes on the probability (axpy_rotated_4's weight)
+                const float w = pw[n] * chunk_levels<KVT>(vc[n], d0, vv);
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] = fmaf(w, vv[i], o[i]);
+            }
+        }
+    }
+    // ---- merge the slots of the wave (lane groups SUB apart) ----
+    xor_up<SUB, 32>([&](auto oc) {
+        constexpr int off = decltype(oc)::value;
+        if constexpr (off >= 16) {  // lane pairs by permlane swaps: f(lower lane's slot, upper lane's slot)
+            float m0, m1, l0, l1;
+            pair_f<off>(m_s, m0, m1);
+            pair_f<off>(l_s, l0, l1);
+            const float M = fmaxf(m0, m1);
+            const bool any = M != -INFINITY;
+            const float a0 = any ? exp2_hw(m0 - M) : 0.0f, a1 = any ? exp2_hw(m1 - M) : 0.0f;
+            l_s = l0 * a0 + l1 * a1;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float o0, o1;
+                pair_f<off>(o[i], o0, o1);
+                o[i] = o0 * a0 + o1 * a1;
+            }
+            m_s = M;
+        } else {
+            const float mo = xor_f<off>(m_s), lo = xor_f<off>(l_s);
+            const float M = fmaxf(m_s, mo);
+            const bool any = M != -INFINITY;
+            const float a1 = any ? exp2_hw(m_s - M) : 0.0f, a2 = any ? exp2_hw(mo - M) : 0.0f;
+            l_s = l_s * a1 + lo * a2;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = o[i] * a1 + xor_f<off>(o[i]) * a2;
+            m_s = M;
+        }
+    });
+    if (lane < SUB) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) wo_s[wv][d0 + i] = o[i];
+    }
+    if (lane == 0) {
+        wm_s[wv] = m_s;
+        wl_s[wv] = l_s;
+    }
+    __syncthreads();
+    // ---- merge the waves, normalize ----
+    if (tid < hd) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, wm_s[w]);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float aw = M != -INFINITY ? exp2_hw(wm_s[w] - M) : 0.0f;
+            O = fmaf(wo_s[w][tid], aw, O);
+            L = fmaf(wl_s[w], aw, L);
+        }
+        o_s[tid] = O * (1.0f / L);
+    }
+    __syncthreads();
+    att_finish<HD, 1, NT>(a, h, o_s);
+}
+
 // merge the ranges of one (token, head); undo the rotation; quantize to Q8_0
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
@@ -1319,8 +1513,13 @@ static void launch_kvt(const AttnArgs &a, dim3 grid, hipStream_t st) {
     }
 }
 
-int attention_splits(int n_tok, int n_kv, int max_len) {
+int attention_splits(int n_tok, int n_kv, int max_len, int hd, bool fused) {
     if (n_tok > 1) return std::max(1, std::min(32, 2048 / std::max(1, n_tok * n_kv)));
+    // one workgroup per query head while the context fits one tile of that kernel
+    // (512 positions at head size 128); with a second tile, a second round trip to
+    // memory, it loses to ranges, and so does a larger tile (more threads per CU do
+    // not fit the registers, fewer threads with more positions each are slower)
+    if (fused && hd > 0 && max_len <= (ATT_HEAD_NT / (hd / 8)) * ATT_HEAD_NP) return 1;
     // single token: about 64 positions per range, the count rounded up to a power
     // of two (so that a captured graph serves a span of context lengths), at most
     // 64 ranges: past 4096 positions the ranges grow instead, since the merge reads
@@ -1354,8 +1553,26 @@ bool attention_fused_ok(const AttnArgs &a) {
            a.n_split >= 1 && a.n_split <= ATT_MAX_SPLIT && (a.n_split & (a.n_split - 1)) == 0;
 }
 
+template <int KVT>
+static void launch_decode_head_kvt(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {
+    const dim3 grid(a.n_head), block(ATT_HEAD_NT);
+    switch (a.hd) {
+    case 64: hipLaunchKernelGGL((attn_decode_head_kernel<KVT, 64>), grid, block, 0, st, a, hp); break;
+    case 128: hipLaunchKernelGGL((attn_decode_head_kernel<KVT, 128>), grid, block, 0, st, a, hp); break;
+    default: hipLaunchKernelGGL((attn_decode_head_kernel<KVT, 256>), grid, block, 0, st, a, hp); break;
+    }
+}
+
 bool launch_attention_fused(const AttnArgs &a, const HeadPrepArgs &hp, hipStream_t st) {
     if (!attention_fused_ok(a) || hp.n_tok != 1) return false;
+    if (a.n_split == 1) {  // one range: one workgroup per query head, no cross-workgroup merge
+        switch (a.kv_type) {
+        case 0: launch_decode_head_kvt<0>(a, hp, st); break;
+        case 1: launch_decode_head_kvt<1>(a, hp, st); break;
+        default: launch_decode_head_kvt<2>(a, hp, st); break;
+        }
+        return true;
+    }
     const int G = a.n_head / a.n_kv;
     const dim3 grid(a.n_split, a.n_kv * (G / decode_heads_per_wg(G)), 1);
     switch (a.kv_type) {

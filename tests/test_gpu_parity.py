@@ -404,7 +404,10 @@ ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32,
 @pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
 def test_attention_shapes_match_oracle(oracle, cuda, hd, nh, nkv, kv):
     """Attention over 300 cached positions (several tiles and context ranges)
-    for head sizes 32..256 and 1..8 query heads per KV head, every cache type."""
+    for head sizes 32..256 and 1..8 query heads per KV head, every cache type.
+    The decode tokens run twice: with the automatic choice (one workgroup per
+    query head at this length where the one-launch path applies) and with the
+    context split into ranges merged across workgroups."""
     from naive_model import max_rel_err
 
     def mut(s):
@@ -423,9 +426,15 @@ def test_attention_shapes_match_oracle(oracle, cuda, hd, nh, nkv, kv):
             err = max_rel_err(lg[t * nv:(t + 1) * nv], lo[t * nv:(t + 1) * nv])
             assert err < tol, f"hd {hd} G {nh // nkv} kv{kv}: batched token {pos + t}: {err}"
         pos = end
+    want = {}
     for t in range(296, 300):  # single-token decode at 296..299 positions of context
-        err = max_rel_err(g.forward([toks[t]], t), o.forward([toks[t]], t))
+        want[t] = o.forward([toks[t]], t)
+        err = max_rel_err(g.forward([toks[t]], t), want[t])
         assert err < tol, f"hd {hd} G {nh // nkv} kv{kv}: decode token {t}: {err}"
+    g.set_attention_ranges(True)  # the same positions again, rewriting their cache rows
+    for t in range(296, 300):
+        err = max_rel_err(g.forward([toks[t]], t), want[t])
+        assert err < tol, f"hd {hd} G {nh // nkv} kv{kv}: decode token {t} over ranges: {err}"
 
 
 PROMPT_ATTN_SHAPES = ATTN_SHAPES + [(64, 4, 2), (96, 6, 6)]
@@ -602,8 +611,9 @@ def test_prompt_attention_kv_splits_match_f64(oracle, cuda, kv):
 
 @pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
 def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv):
-    """Single-token attention (the fused launch: prep, append, context ranges,
-    range merge; groups of 6 and 8 query heads split in two workgroups) at
+    """Single-token attention (the fused launch: prep, append and attention, one
+    workgroup per query head at this length, and again with context ranges and
+    the range merge; groups of 6 and 8 query heads split in two workgroups) at
     positions 296..299 against a float64 evaluation of cpu.rs:550-634 on the
     prepared queries and the f16 cache rows, to the f32 bound of the prompt
     test above."""
@@ -616,7 +626,8 @@ def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv
     for pos in range(0, 296, 64):
         g.forward(toks[pos:min(pos + 64, 296)], pos)
     g.set_capture(True)
-    for p in range(296, 300):
+    for ranges, p in [(r, p) for r in (False, True) for p in range(296, 300)]:
+        g.set_attention_ranges(ranges)
         g.forward([toks[p]], p)
         for layer in range(spec.n_layer):
             q = g.capture(layer, 3, qd).reshape(nh, hd).astype(np.float64)
@@ -633,7 +644,7 @@ def test_decode_attention_matches_f64_on_captured_rows(oracle, cuda, hd, nh, nkv
                 err = np.max(np.abs(att[hq] - ref))
                 vmax = np.max(np.abs(V[kv, :p + 1]))
                 assert err <= (8 * 2.0 ** -24 * np.max(np.abs(s)) + 5e-6) * vmax + 1e-6, \
-                    f"hd {hd} G {G} layer {layer} token {p} head {hq}: {err}"
+                    f"hd {hd} G {G} layer {layer} token {p} head {hq} ranges {ranges}: {err}"
 
 
 @pytest.mark.parametrize("kv", [0, 1, 2])
@@ -673,9 +684,11 @@ def test_kv_codes_bit_exact_on_identical_inputs(oracle, cuda, kv):
 @pytest.mark.parametrize("kv", [0, 1, 2])
 @pytest.mark.parametrize("arch", ["llama", "qwen3"])
 def test_long_decode_matches_oracle(oracle, cuda, arch, kv):
-    """132 single-token steps (query/key prep, cache append, attention and the
-    range merge in one launch) from position 8 to 139: every context length
-    across tile and range boundaries, against the oracle."""
+    """132 single-token steps (query/key prep, cache append and attention in one
+    launch) from position 8 to 139: every context length across tile and range
+    boundaries, against the oracle.  Odd positions run the context-range kernel
+    with its range merge, even ones one workgroup per query head, so each reads
+    cache rows the other appended."""
     from naive_model import max_rel_err
     spec, g, o = _pair(oracle, arch, Q8_0, kv, n_ctx=160, max_batch=8)
     nv = spec.n_vocab
@@ -684,6 +697,7 @@ def test_long_decode_matches_oracle(oracle, cuda, arch, kv):
     o.forward(toks[:8], 0)
     tol = 0.03 if kv == 0 else 0.05
     for pos in range(8, 140):
+        g.set_attention_ranges(pos % 2 == 1)
         err = max_rel_err(g.forward([toks[pos]], pos), o.forward([toks[pos]], pos))
         assert err < tol, f"{arch} kv{kv}: decode position {pos}: {err}"
 
