@@ -12,13 +12,15 @@ BLOCK = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22)
 _SCALAR_SIZE = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
 
 
-def tensor_table(img) -> dict:
-    """name -> (ggml type, dims (cols first), stored bytes)"""
+def _parse(img):
+    """(metadata alignment, [(name, ggml type, dims, offset in the data region)],
+    end of the tensor infos)"""
     b = memoryview(img).cast("B")
     magic, _version, n_t, n_kv = struct.unpack_from("<IIQQ", b, 0)
     if magic != 0x46554747:
         raise ValueError("not a GGUF image")
     pos = 24
+    align = 32
 
     def skip(ty, pos):
         if ty in _SCALAR_SIZE:
@@ -37,10 +39,13 @@ def tensor_table(img) -> dict:
 
     for _ in range(n_kv):
         klen = struct.unpack_from("<Q", b, pos)[0]
+        key = bytes(b[pos + 8:pos + 8 + klen])
         pos += 8 + klen
         ty = struct.unpack_from("<I", b, pos)[0]
+        if key == b"general.alignment" and ty == 4:  # u32 (gguf.rs:256-258)
+            align = struct.unpack_from("<I", b, pos + 4)[0]
         pos = skip(ty, pos + 4)
-    out = {}
+    infos = []
     for _ in range(n_t):
         nlen = struct.unpack_from("<Q", b, pos)[0]
         name = bytes(b[pos + 8:pos + 8 + nlen]).decode()
@@ -48,14 +53,34 @@ def tensor_table(img) -> dict:
         nd = struct.unpack_from("<I", b, pos)[0]
         dims = list(struct.unpack_from(f"<{nd}Q", b, pos + 4))
         pos += 4 + 8 * nd
-        ty = struct.unpack_from("<I", b, pos)[0]
-        pos += 12  # type, offset
+        ty, off = struct.unpack_from("<IQ", b, pos)
+        pos += 12
+        infos.append((name, ty, dims, off))
+    return align, infos, pos
+
+
+def tensor_table(img) -> dict:
+    """name -> (ggml type, dims (cols first), stored bytes)"""
+    out = {}
+    for name, ty, dims, _off in _parse(img)[1]:
         n = 1
         for d in dims:
             n *= d
         bs, bb = BLOCK[ty]
         out[name] = (ty, dims, n // bs * bb)
     return out
+
+
+def tensor_offset(img, name: str) -> int:
+    """byte offset of a tensor's data in the image: the data region starts at the
+    end of the tensor infos rounded up to general.alignment (32 by default,
+    gguf.rs:256-262)"""
+    align, infos, end = _parse(img)
+    start = (end + align - 1) // align * align
+    for n, _ty, _dims, off in infos:
+        if n == name:
+            return start + off
+    raise KeyError(name)
 
 
 def per_token_costs(img, n_expert_used: int = 0) -> dict:

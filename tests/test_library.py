@@ -199,3 +199,19 @@ def test_baseline_moe_image(oracle):
     w = G.dequantize(ty, raw[: 2 * per_expert], 2 * 768 * 2048)  # the first two experts
     assert ty == synth.Q4_K and list(dims) == [2048, 768, 128] and abs(w.std() - 0.02) < 0.002
     assert g.tensors["output.weight"][0] == synth.Q6_K and g.tensors["token_embd.weight"][0] == synth.Q6_K
+
+
+def test_tensor_offset_matches_independent_reader():
+    """gguf.tensor_offset (the data region start rounded to general.alignment plus
+    the tensor's offset, gguf.rs:256-262) against tests/gguf_np.py's reader, for
+    every tensor of two tiny images."""
+    import numpy as np
+    from gguf_np import GGUF
+    from rust_interference_engine_amd import gguf
+    for spec in (synth.tiny("qwen3", synth.Q4_0), synth.tiny("llama", synth.Q4_K)):
+        img = synth.build(spec)
+        ref = GGUF(img)
+        buf = np.frombuffer(img, np.uint8)
+        for name, (_ty, _dims, data) in ref.tensors.items():
+            off = gguf.tensor_offset(img, name)
+            assert np.array_equal(buf[off:off + len(data)], np.frombuffer(data, np.uint8)), name
