@@ -642,8 +642,9 @@ __device__ __forceinline__ void query_registers(const AttnArgs &a, int G, int hd
     }
 }
 
-// K and V chunks of NP positions tile + pi + PP·n (rows past r1 repeat row r0)
-template <int KVT, int PP, int NP = ATT_NP>
+// K and V chunks of NP positions tile + pi + PP·n (rows past r1 repeat row r0);
+// LOADK false: V only (the K rows are loaded in the matrix-core layout instead)
+template <int KVT, int PP, int NP = ATT_NP, bool LOADK = true>
 __device__ __forceinline__ void load_tile(const AttnArgs &a, size_t kv_row0, int tile, int pi, int r0, int r1, int hd, int d0, int tb,
                                           KvChunk<KVT> (&kc)[NP], KvChunk<KVT> (&vc)[NP], bool (&ok)[NP]) {
 #pragma unroll
@@ -652,9 +653,85 @@ __device__ __forceinline__ void load_tile(const AttnArgs &a, size_t kv_row0, int
         ok[n] = pos < r1;
         const int q = ok[n] ? pos : r0;
         const size_t row = kv_row0 + (size_t)(q < a.slots ? q : q % a.slots);
-        load_chunk<KVT>(a.k_cache, a.k_scale, row, hd, d0, tb, kc[n]);
+        if constexpr (LOADK) load_chunk<KVT>(a.k_cache, a.k_scale, row, hd, d0, tb, kc[n]);
         load_chunk<KVT>(a.v_cache, a.v_scale, row, hd, d0, tb, vc[n]);
     }
+}
+
+// ---- Turbo4 scores on int8 matrix cores (head size 128, the range kernel) ----
+// The 16 positions of a wave's tile (slot 4w + s, pass n: position tile + 4w + s +
+// 16n) are the rows r = 4n + s of v_mfma_i32_16x16x32_i8, one MFMA per 32-value
+// chunk c: A = the K rows' levels (lane l: row l % 16, chunk values 8·(l / 16) ..
+// +7, i.e. bytes 16c + 8·(l/16 & 1) of the code row, high nibbles for l/16 ≥ 2),
+// B = the rotated Q8_0 query codes (lane l: query head l % 16 of the slice, the
+// same 8 chunk values), D = the exact int32 chunk dots Σ LEVEL[code]·q8 of
+// dot_rotated_4 (turbo.rs:178-193; lane l: head l % 16, rows 4·(l/16) + i).
+// score = Σ_c (d_q,c · scale/46) · dot_c, as the VALU path forms each chunk's term.
+typedef int att_v4i __attribute__((ext_vector_type(4)));
+struct KTileMF {
+    uint2 w[4];      // the A row's code bytes of chunks 0..3
+    uint32_t sc[4];  // f16 scales of the lane's output rows 4·(l/16) + i
+};
+__device__ __forceinline__ int ktile_row_pos(int tile, int wv, int r) { return tile + 4 * wv + (r & 3) + 16 * (r >> 2); }
+__device__ __forceinline__ void load_k_mfma(const AttnArgs &a, size_t kv_row0, int tile, int wv, int lane, int r0, int r1, KTileMF &k) {
+    const int kg = lane >> 4;
+    const int pos = ktile_row_pos(tile, wv, lane & 15);
+    const int q = pos < r1 ? pos : r0;
+    const size_t row = kv_row0 + (size_t)(q < a.slots ? q : q % a.slots);
+    const uint8_t *src = a.k_cache + row * 64 + 8 * (kg & 1);
+#pragma unroll
+    for (int c = 0; c < 4; c++) k.w[c] = *(const uint2 *)(src + 16 * c);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int op = ktile_row_pos(tile, wv, 4 * kg + i);
+        const int oq = op < r1 ? op : r0;
+        k.sc[i] = a.k_scale[kv_row0 + (size_t)(oq < a.slots ? oq : oq % a.slots)];  // one scale per row (block 128)
+    }
+}
+// the new position's row from the LDS mirror (row bytes, then the f16 scale at KV_MIRROR_SC)
+__device__ __forceinline__ void k_mfma_mirror(int tile, int wv, int lane, int p, const uint8_t *mirror, KTileMF &k) {
+    const int kg = lane >> 4;
+    if (ktile_row_pos(tile, wv, lane & 15) == p) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) k.w[c] = *(const uint2 *)(mirror + 16 * c + 8 * (kg & 1));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (ktile_row_pos(tile, wv, 4 * kg + i) == p) k.sc[i] = *(const uint16_t *)(mirror + KV_MIRROR_SC);
+}
+// scores of the wave's 16 positions × MG heads, handed to the slot layout through
+// LDS (sc_s: [64 rows][MG]); sc[n][j] for this lane's slot s, pass n, head j
+template <int MG>
+__device__ __forceinline__ void mfma_scores(const KTileMF &k, const long (&qb)[4], const float (&qdc)[4], int wv, int lane, float *sc_s,
+                                            float (&sc)[ATT_NP][MG]) {
+    const int kg = lane >> 4, hh = lane & 15;
+    att_v4i I[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t c0 = (kg >= 2 ? (k.w[c].x >> 4) : k.w[c].x) & 0x0F0F0F0Fu;
+        const uint32_t c1 = (kg >= 2 ? (k.w[c].y >> 4) : k.w[c].y) & 0x0F0F0F0Fu;
+        const long av = (long)(((unsigned long)lut16(c1, KV_LV0, KV_LV1, KV_LV2, KV_LV3) << 32) |
+                               (unsigned long)lut16(c0, KV_LV0, KV_LV1, KV_LV2, KV_LV3));
+        const att_v4i z = {0, 0, 0, 0};
+        I[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[c], z, 0, 0, 0);
+    }
+    if (hh < MG) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float ks = h2f(k.sc[i]) * (1.0f / 46.0f);
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc += (qdc[c] * ks) * (float)I[c][i];
+            sc_s[(16 * wv + 4 * kg + i) * MG + hh] = acc;
+        }
+    }
+    wave_sync();
+    const int s = (lane >> 4);  // the slot within the wave (16 lanes per cache row at head size 128)
+#pragma unroll
+    for (int n = 0; n < ATT_NP; n++)
+#pragma unroll
+        for (int j = 0; j < MG; j++) sc[n][j] = sc_s[(16 * wv + 4 * n + s) * MG + j];
+    wave_sync();
 }
 
 // Prompt tokens: one workgroup per (range, kv head, token); per tile of positions
@@ -986,7 +1063,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
             prep_load_fast<HD>(hp, kind, kind == 0 ? h0 + v : g, p, pin[i]);
         }
     }
-    load_tile<KVT, PP>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // every row index is in range (mod slots)
+    constexpr bool MFK = KVT == 2 && HD == 128;  // Turbo4 scores on int8 matrix cores
+    load_tile<KVT, PP, ATT_NP, !MFK>(a, kv_row0, r0, pi, r0, r1, hd, d0, tb, kc, vc, ok);  // every row index is in range (mod slots)
+    KTileMF kt;
+    if constexpr (MFK) load_k_mfma(a, kv_row0, r0, wv, lane, r0, r1, kt);
     if (fast) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -1005,6 +1085,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     uint32_t qq[MG][2];
     float qdd[MG];
     query_registers<KVT, MG>(a, H, hd, tb, d0, qs_f, qs_i, qs_d, qf, qq, qdd);
+    long qb[4] = {0, 0, 0, 0};  // MFK: B operands, lane l: head l % 16, chunk values 8·(l/16)..+7
+    float qdc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    __shared__ float sc_s[MFK ? 64 * MG : 1];
+    if constexpr (MFK) {
+        const int hh = lane & 15, kg = lane >> 4;
+        if (hh < H) {
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                qb[cc] = *(const long *)(qs_i + hh * hd + 32 * cc + 8 * kg);
+                qdc[cc] = qs_d[hh * 4 + cc];
+            }
+        }
+    }
 
     float m_s[MG], l_s[MG], o[MG][8];
 #pragma unroll
@@ -1016,17 +1109,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     }
     const bool softcap = a.softcap > 0.0f;
     for (int tile = r0; tile < r1; tile += TP) {
-        if (tile != r0) load_tile<KVT, PP>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
+        if (tile != r0) {
+            load_tile<KVT, PP, ATT_NP, !MFK>(a, kv_row0, tile, pi, r0, r1, hd, d0, tb, kc, vc, ok);
+            if constexpr (MFK) load_k_mfma(a, kv_row0, tile, wv, lane, r0, r1, kt);
+        }
         if (own && tile + TP >= r1) {
 #pragma unroll
             for (int n = 0; n < ATT_NP; n++)
                 if (tile + pi + PP * n == p) {
-                    load_chunk<KVT>(mirror[0], (const uint16_t *)(mirror[0] + KV_MIRROR_SC), 0, hd, d0, tb, kc[n]);
+                    if constexpr (!MFK) load_chunk<KVT>(mirror[0], (const uint16_t *)(mirror[0] + KV_MIRROR_SC), 0, hd, d0, tb, kc[n]);
                     load_chunk<KVT>(mirror[1], (const uint16_t *)(mirror[1] + KV_MIRROR_SC), 0, hd, d0, tb, vc[n]);
                 }
+            if constexpr (MFK) k_mfma_mirror(tile, wv, lane, p, mirror[0], kt);
         }
         float sc[ATT_NP][MG];
-        tile_scores<KVT, SUB, MG>(kc, qf, qq, qdd, c, cact, d0, sc);
+        if constexpr (MFK) mfma_scores<MG>(kt, qb, qdc, wv, lane, sc_s, sc);
+        else tile_scores<KVT, SUB, MG>(kc, qf, qq, qdd, c, cact, d0, sc);
         if (softcap) {  // uniform
 #pragma unroll
             for (int n = 0; n < ATT_NP; n++)
