@@ -293,6 +293,30 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
         }
         load_pass(base0);  // unconditional, as above
     }
+    // F32 weights with a norm input up to 4096 wide (the MoE router): x and the norm
+    // weight are requested before the weight stream, as in the PRO8 prologue, so the
+    // prologue's loads do not wait behind the weights (loads complete in issue order)
+    constexpr int FX = 4;  // float4 of x per thread for the sum of squares
+    float4 fx[FX], ux[UPL][2], uw[UPL][2];
+    const bool f32pro = TY == T_F32 && p.nin.x && p.nin.w && p.K <= 4096;
+    if constexpr (TY == T_F32) {
+        if (f32pro) {
+#pragma unroll
+            for (int k = 0; k < FX; k++) {
+                const int i0 = p.nin.order16 ? 16 * tid + 4 * k : 4 * tid + 1024 * k;
+                const bool in = tid < 256 && (p.nin.order16 ? 16 * tid : i0) < p.K;
+                fx[k] = in ? *(const float4 *)(p.nin.x + i0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const float4 *xp = (const float4 *)(p.nin.x + 8 * uu[k]), *wp = (const float4 *)(p.nin.w + 8 * uu[k]);
+                ux[k][0] = xp[0];
+                ux[k][1] = xp[1];
+                uw[k][0] = wp[0];
+                uw[k][1] = wp[1];
+            }
+        }
+    }
     if constexpr (!PRO8 && !PROQ) {
         if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
     }
@@ -465,7 +489,30 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
         }
     }
     if constexpr (TY == T_F32) {
-        if (p.nin.x) {
+        if (f32pro) {  // the same arithmetic on the early loads; the barrier orders LDS only
+            __shared__ float s_red2[4];
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FX; k++) {
+                ss = fmaf(fx[k].x, fx[k].x, ss);
+                ss = fmaf(fx[k].y, fx[k].y, ss);
+                ss = fmaf(fx[k].z, fx[k].z, ss);
+                ss = fmaf(fx[k].w, fx[k].w, ss);
+            }
+            ss = wave_sum(ss, 64);
+            if ((tid & 63) == 0 && tid < 256) s_red2[tid >> 6] = ss;
+            lds_barrier();
+            const float scale = 1.0f / sqrtf(((s_red2[0] + s_red2[1]) + (s_red2[2] + s_red2[3])) / (float)p.K + p.nin.eps);
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const float4 x0 = ux[k][0], x1 = ux[k][1], w0 = uw[k][0], w1 = uw[k][1];
+                a[k].f[0] = x0.x * scale * w0.x; a[k].f[1] = x0.y * scale * w0.y;
+                a[k].f[2] = x0.z * scale * w0.z; a[k].f[3] = x0.w * scale * w0.w;
+                a[k].f[4] = x1.x * scale * w1.x; a[k].f[5] = x1.y * scale * w1.y;
+                a[k].f[6] = x1.z * scale * w1.z; a[k].f[7] = x1.w * scale * w1.w;
+            }
+            have_act = true;
+        } else if (p.nin.x) {
             // The activation is RMSNorm(x)·w in f32, bit for bit the rows of the
             // standalone kernel it replaces: the scale from that kernel's partial
             // sums (the first 256 threads; q8_0_rows_kernel's 16 consecutive values
@@ -576,7 +623,6 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
 // agent-scope acquire, re-arms the counter and runs the routing in its first wave.
 __device__ __forceinline__ void route_last_workgroup(const DecP &p) {
     __shared__ int s_last;
-    __shared__ __align__(16) float s_ps[64 * 8];
     __syncthreads();  // the workgroup's logits are stored
     if (threadIdx.x == 0) {
         const int old = __hip_atomic_fetch_add(p.route.cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -588,7 +634,7 @@ __device__ __forceinline__ void route_last_workgroup(const DecP &p) {
     }
     __syncthreads();
     if (s_last && threadIdx.x < 64)
-        moe_route_wave(p.seg[0].out, p.route.n_exp, p.route.k, p.route.norm_topk, p.route.unit_weights, p.route.sel, p.route.wgt, s_ps);
+        moe_route_wave(p.seg[0].out, p.route.n_exp, p.route.k, p.route.norm_topk, p.route.unit_weights, p.route.sel, p.route.wgt);
 }
 
 template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false, bool PROQ = false>

@@ -158,9 +158,8 @@ void launch_quant_only(const float *x, int ldx, int n_rows, int K, int fmt, cons
 // MoE routing: one wavefront per token (moe_route_wave, moe_route.hpp)
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_exp, int k, int norm_topk, int unit_weights, int *sel,
                                                        float *wgt) {
-    __shared__ __align__(16) float ps[64 * 8];
     const size_t t = blockIdx.x;
-    moe_route_wave(logits + t * n_exp, n_exp, k, norm_topk, unit_weights, sel + t * k, wgt + t * k, ps);
+    moe_route_wave(logits + t * n_exp, n_exp, k, norm_topk, unit_weights, sel + t * k, wgt + t * k);
 }
 
 // out[t] (= or +=) Σ_j w[t][j]·y[t·k + j], j in ascending expert order, starting from 0

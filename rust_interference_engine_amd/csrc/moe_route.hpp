@@ -11,7 +11,7 @@ namespace rie {
 // top k, optionally renormalize by their sum taken in sorted order.
 // One wave per token: lane l holds experts l + 64i (n_exp ≤ 512, checked by the
 // host).  The softmax sum runs over the experts in order, sequentially, like the
-// reference's (ops.rs:38-49), by one lane over an LDS copy.  Top-k is k rounds:
+// reference's (ops.rs:38-49): one chain of adds over readlane values.  Top-k is k rounds:
 // the maximum of the experts not yet taken (DPP within 16-lane rows, then the
 // four row maxima), and of the experts holding it the lowest index (ballots in
 // expert order), which is the reference's index tie-break (cpu.rs:495).  Lane j
@@ -25,10 +25,9 @@ __device__ __forceinline__ float row_max16(float v) {
     return fmaxf(v, dpp_f<DPP_ROW_ROR8>(v));
 }
 // One wavefront routes one token: l holds its n_exp logits; sel/wgt receive its k
-// choices in ascending expert order; ps is 64·8 floats of LDS.
-__device__ __forceinline__ void moe_route_wave(const float *l, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
-                                               float *ps) {
-    constexpr int NE = 8;
+// choices in ascending expert order.  NE = experts per lane (n_exp ≤ 64·NE).
+template <int NE>
+__device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt) {
     const int lane = threadIdx.x & 63;
     float pr[NE];
     float mx = -INFINITY;
@@ -40,24 +39,16 @@ __device__ __forceinline__ void moe_route_wave(const float *l, int n_exp, int k,
     }
     mx = wave_max(mx, 64);
 #pragma unroll
-    for (int i = 0; i < NE; i++) {
-        pr[i] = lane + 64 * i < n_exp ? expf(pr[i] - mx) : 0.0f;
-        ps[lane + 64 * i] = pr[i];
-    }
-    wave_sync();
-    float s_inv = 0.0f;
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int e0 = 0; e0 < n_exp; e0 += 4) {  // n_exp % 4 == 0 is not assumed: the pad holds zeros
-            const float4 q = *(const float4 *)(ps + e0);
-            sum += q.x;
-            if (e0 + 1 < n_exp) sum += q.y;
-            if (e0 + 2 < n_exp) sum += q.z;
-            if (e0 + 3 < n_exp) sum += q.w;
-        }
-        s_inv = 1.0f / sum;
-    }
-    const float inv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_inv)));
+    for (int i = 0; i < NE; i++) pr[i] = lane + 64 * i < n_exp ? expf(pr[i] - mx) : 0.0f;
+    // the sum over the experts in order, one add at a time (expert e sits in lane
+    // e mod 64, register e / 64): the same chain in every lane, through readlane;
+    // the zeros past n_exp add nothing
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NE; i++)
+#pragma unroll
+        for (int ln = 0; ln < 64; ln++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[i]), ln));
+    const float inv = 1.0f / sum;
 #pragma unroll
     for (int i = 0; i < NE; i++) pr[i] *= inv;
     uint32_t taken = 0;  // bit i: expert lane + 64i is chosen
@@ -92,6 +83,12 @@ __device__ __forceinline__ void moe_route_wave(const float *l, int n_exp, int k,
         sel[rank] = my_c;
         wgt[rank] = unit_weights ? 1.0f : my_v / norm;
     }
+}
+__device__ __forceinline__ void moe_route_wave(const float *l, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt) {
+    if (n_exp <= 64) moe_route_wave_t<1>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else if (n_exp <= 128) moe_route_wave_t<2>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else if (n_exp <= 256) moe_route_wave_t<4>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else moe_route_wave_t<8>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
 }
 
 
