@@ -201,6 +201,10 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     d_kcap_ = dalloc<float>(allocs_, mb * kvd);
     d_att_ = dalloc<float>(allocs_, mb * qd);
     d_o_ = dalloc<float>(allocs_, mb * E);
+    // partial sums of K-split prompt GEMMs (up to three planes of a batch's E-wide
+    // outputs, at most 64 MiB): only batches above 64 tokens split
+    gemm_ws_cap_ = mb > 64 ? std::min<size_t>(3 * mb * E, (size_t)1 << 24) : 0;
+    if (gemm_ws_cap_) d_gemm_ws_ = dalloc<float>(allocs_, gemm_ws_cap_);
     // routed experts per token as the layers run them (clamped to [1, n_expert], model/mod.rs:176)
     const size_t nu = std::max<size_t>(n_used_max_, 1);
     d_h_ = dalloc<float>(allocs_, mb * ff_max_ * nu);
@@ -328,7 +332,7 @@ void HipBackend::matmul(const GemvSeg *segs, int nseg, int n, int K, const ActQ8
         while (n > 8 && s < j && gemm_supported(segs[s].w.ty, K)) {
             int e = s + 1;
             while (e < j && e - s < 3 && segs[e].w.ty == segs[s].w.ty) e++;
-            if (!launch_gemm(&segs[s], e - s, a, n, K, st_)) break;
+            if (!launch_gemm(&segs[s], e - s, a, n, K, st_, nullptr, d_gemm_ws_, gemm_ws_cap_)) break;
             s = e;
         }
         if (s < j && !launch_gemv(&segs[s], j - s, a, d_xn_, n, K, st_))
@@ -351,7 +355,7 @@ void HipBackend::ffn_dense(const DevLayer &L, int n, float *out, int epi) {
     }
     const ActQ8 &a = act_format(L.gate.ty) == ACT_Q8K ? actk_ : act0_;
     bool done = false;
-    if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
+    if (n > 8 && gemm_supported(L.gate.ty, E)) done = launch_gemm_glu(L.gate, L.up, a, n, E, d_h_, ff, c.gelu, nullptr, st_);
     const int fmt = act_format(L.down.ty);
     // single-token Q8_0 down projection: the gate/up kernel quantizes h itself
     bool h_quantized = false;
@@ -593,7 +597,7 @@ void HipBackend::expert_ffn(const DevWeight &g, const DevWeight &u, const DevWei
     prepare(x, nullptr, m, E, ws, 2, false);
     const ActQ8 &a = act_format(g.ty) == ACT_Q8K ? actk_ : act0_;
     bool done = false;
-    if (m > 8 && gemm_supported(g.ty, E)) done = launch_gemm_glu(g, u, a, m, E, d_h_, ff, c.gelu, d_gemm_ws_, st_);
+    if (m > 8 && gemm_supported(g.ty, E)) done = launch_gemm_glu(g, u, a, m, E, d_h_, ff, c.gelu, nullptr, st_);
     if (!done && !launch_gemv_glu(g, u, a, d_xn_, m, E, d_h_, ff, c.gelu, nullptr, st_))
         throw Error{E_UNSUPPORTED, "unsupported: expert FFN weights"};
     const int fmt = act_format(dn.ty);

@@ -7,6 +7,7 @@
 #include "backend.hpp"
 #include "synth.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
@@ -276,10 +277,17 @@ int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
         a.isum = const_cast<int32_t *>(isum);
         a.bsums = const_cast<int16_t *>(bsums);
         rie::GemvSeg sg{mkw(ty, w, rows, k), out, rows, rie::EPI_STORE};
-        if (!rie::gemm_supported(ty, (size_t)k) || !rie::launch_gemm(&sg, 1, a, n_tok, k, 0))
-            throw Error{rie::E_UNSUPPORTED, "no GEMM kernel for this weight type/shape"};
-        RIE_HIP_CHECK(hipGetLastError());
-        RIE_HIP_CHECK(hipDeviceSynchronize());
+        // room for the partial sums of a K split (three planes), as the backend has
+        const size_t cap = 3 * (size_t)std::max(n_tok, 0) * (size_t)std::max(rows, 0);
+        float *part = nullptr;
+        if (cap) RIE_HIP_CHECK(hipMalloc(&part, cap * sizeof(float)));
+        const bool ok = rie::gemm_supported(ty, (size_t)k) && rie::launch_gemm(&sg, 1, a, n_tok, k, 0, nullptr, part, cap);
+        hipError_t e = hipGetLastError();
+        hipError_t e2 = hipDeviceSynchronize();
+        if (part) (void)hipFree(part);
+        if (!ok) throw Error{rie::E_UNSUPPORTED, "no GEMM kernel for this weight type/shape"};
+        RIE_HIP_CHECK(e);
+        RIE_HIP_CHECK(e2);
     });
 }
 

@@ -188,7 +188,9 @@ bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 
 // ---- gemm.hip (prefill, int8 MFMA) ----
 bool gemm_supported(int ty, size_t K);
 // grp: one segment per expert group (the segment's rows are one expert's; see GroupTiles)
-bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr);
+// part (part_cap floats): room for the partial sums of a K split (see launch_t)
+bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr,
+                 float *part = nullptr, size_t part_cap = 0);
 bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
                      float *scratch, hipStream_t st, const GroupTiles *grp = nullptr);
 

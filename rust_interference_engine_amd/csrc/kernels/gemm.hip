@@ -49,6 +49,13 @@ struct GemmP {
     int n_tok, K;
     int grouped;    // expert groups: one matrix per expert (grp), 64-token tiles from its table
     GroupTiles grp;
+    // K split (one segment, not gated or grouped): split 0 runs the segment's
+    // epilogue on its partial sum, split i > 0 stores its partial to part[i-1]
+    // ([n_tok][ld], stride part_stride floats), which a second launch adds to the
+    // output in split order
+    int ks;
+    float *part;
+    size_t part_stride;
 };
 
 // A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
@@ -190,8 +197,10 @@ __global__ __launch_bounds__(256, (!GLU && NT == 1) ? 3 : 2) void gemm_kernel(Ge
     const int wv = tid >> 6, l = tid & 63;
     const int wr = wv >> 1, wc = wv & 1;
     // workgroups of one row group share an XCD (id mod 8) and are dispatched together
+    // (the K splits of one tile are neighbours in u: the same XCD)
     const int bid = blockIdx.x;
-    const int xcd = bid & 7, u = bid >> 3;
+    const int xcd = bid & 7, uk = bid >> 3;
+    const int ksi = uk % p.ks, u = uk / p.ks;
     const int tg = u % p.n_tg;
     const int rg = (u / p.n_tg) * 8 + xcd;
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
@@ -224,12 +233,15 @@ __global__ __launch_bounds__(256, (!GLU && NT == 1) ? 3 : 2) void gemm_kernel(Ge
     // two stages before their LDS store.  Load indices past the last stage repeat the
     // last stage and the step count is even, so every load is unconditional and the
     // compiler's wait for a register set counts exactly the loads issued after it.
-    const int n_stages = p.K / (32 * G_KC);
+    // this workgroup's stages: [k0, k0 + n_stages) of the K / 128 (its K split)
+    const int all_stages = p.K / (32 * G_KC);
+    const int k0 = ksi * all_stages / p.ks;
+    const int n_stages = (ksi + 1) * all_stages / p.ks - k0;
     const int last_stage = n_stages - 1;
     StageRegs<TY, GLU, BN> ra, rb;
-    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, tid, ra);
+    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, k0 * G_KC, tid, ra);
     stage_store<TY, GLU, BN>(st[0], tid, ra);
-    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, min(1, last_stage) * G_KC, tid, rb);
+    stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, (k0 + min(1, last_stage)) * G_KC, tid, rb);
     __syncthreads();
     // Per stage: all operands of the stage's KC blocks from LDS, then the
     // P = KC·NT·NW tile products in a software pipeline: the MFMAs of product
@@ -237,7 +249,7 @@ __global__ __launch_bounds__(256, (!GLU && NT == 1) ? 3 : 2) void gemm_kernel(Ge
     constexpr int P = G_KC * NT * NW;
     // rl: receives stage s + 2; rs: holds stage s + 1, stored to LDS after stage s
     auto body = [&](int s, StageRegs<TY, GLU, BN> &rl, const StageRegs<TY, GLU, BN> &rs) {
-        stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, min(s + 2, last_stage) * G_KC, tid, rl);
+        stage_load<TY, GLU, BN>(p, sg, row0, tokA, tokD, woff, (k0 + min(s + 2, last_stage)) * G_KC, tid, rl);
         if (s < n_stages) {  // workgroup-uniform; the idle step of an odd stage count skips it
             const GemmStage<TY, GLU, BN> &S = st[s & 1];
             v4i bw[G_KC][NW], av[G_KC][NT];
@@ -308,9 +320,9 @@ __global__ __launch_bounds__(256, (!GLU && NT == 1) ? 3 : 2) void gemm_kernel(Ge
     const int rows = p.rows[sg];
     const int row = row0 + wrow;
     if (row >= rows) return;
-    float *out = p.out[sg];
     const int ld = p.ld[sg];
-    const int epi = p.epi[sg];
+    float *out = ksi ? p.part + (size_t)(ksi - 1) * p.part_stride : p.out[sg];
+    const int epi = ksi ? EPI_STORE : p.epi[sg];
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
@@ -330,13 +342,36 @@ bool gemm_supported(int ty, size_t K) {
     return ((ty == T_Q4_0 || ty == T_Q8_0) && K % (32 * G_KC) == 0 && K > 0) || gemm_kq_supported(ty, K);
 }
 
+// out[t·ld + r] += part[0][…] + … + part[n_part−1][…] for r < rows, in split order
+__global__ __launch_bounds__(256) void gemm_add_parts_kernel(float *__restrict__ out, const float *__restrict__ part, size_t stride,
+                                                             int n_part, int rows, int ld) {
+    const int r = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (r >= rows) return;
+    const size_t i = (size_t)t * ld + r;
+    float v = out[i];
+    for (int k = 0; k < n_part; k++) v += part[(size_t)k * stride + i];
+    out[i] = v;
+}
+
 // 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
-// then 64-token tiles (one 32-token tile per wave); the gated pair always 64
+// then 64-token tiles (one 32-token tile per wave); the gated pair always 64.
+// One segment with a long K (≥ 64 stages of 128) whose 128-token tiles number
+// under 512 keeps the 128-token tiles and splits K in 2 or 4 (each split ≥ 16
+// stages) while part holds the extra splits' partial sums (part_cap floats).
 template <int TY, bool GLU>
-static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp) {
+static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp, float *part, size_t part_cap) {
     const int slots = (p.n_rg + 7) / 8;
+    const int tiles128 = slots * 8 * ((p.n_tok + 127) / 128);
+    const int n_st = p.K / (32 * G_KC);
+    p.ks = 1;
+    if (!GLU && !grp && p.nseg == 1 && part && n_st >= 64 && p.n_tok > 64) {
+        const size_t plane = (size_t)p.n_tok * p.ld[0];
+        while (p.ks < 4 && tiles128 * p.ks < 512 && n_st / (2 * p.ks) >= 16 && (size_t)(2 * p.ks - 1) * plane <= part_cap) p.ks *= 2;
+        p.part = part;
+        p.part_stride = plane;
+    }
     int nt = 2;
-    if (GLU || (slots * 8 * ((p.n_tok + 127) / 128) < 512 && p.n_tok > 64)) nt = 1;  // GLU: two register sets of 128-token stages do not fit
+    if (GLU || (p.ks == 1 && tiles128 < 512 && p.n_tok > 64)) nt = 1;  // GLU: two register sets of 128-token stages do not fit
     p.n_tg = (p.n_tok + 64 * nt - 1) / (64 * nt);
     if (grp) {  // 64-token tiles from the grouping's table
         static_assert(GROUP_BN == 64, "grouped tiles are one 32-token tile per wave");
@@ -345,13 +380,16 @@ static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp) {
         p.grp = *grp;
         p.n_tg = grp->max_tiles;
     }
+    const dim3 grid(slots * 8 * p.n_tg * p.ks);
     if constexpr (!GLU) {
-        if (nt == 2) {
-            hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
-            return;
-        }
+        if (nt == 2) hipLaunchKernelGGL((gemm_kernel<TY, GLU, 2>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), grid, dim3(256), 0, st, p);
+        if (p.ks > 1)
+            hipLaunchKernelGGL(gemm_add_parts_kernel, dim3((p.rows[0] + 255) / 256, p.n_tok), dim3(256), 0, st, p.out[0], p.part,
+                               p.part_stride, p.ks - 1, p.rows[0], p.ld[0]);
+        return;
     }
-    hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), grid, dim3(256), 0, st, p);
 }
 
 static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }
@@ -365,7 +403,8 @@ static void set_groups(GemmP &p, int nseg) {
     p.n_rg = acc;
 }
 
-bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp) {
+bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp, float *part,
+                 size_t part_cap) {
     if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act) || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
     if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st, grp);
@@ -387,8 +426,8 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (ty == T_Q4_0) launch_t<T_Q4_0, false>(p, st, grp);
-    else launch_t<T_Q8_0, false>(p, st, grp);
+    if (ty == T_Q4_0) launch_t<T_Q4_0, false>(p, st, grp, part, part_cap);
+    else launch_t<T_Q8_0, false>(p, st, grp, part, part_cap);
     return true;
 }
 
@@ -416,8 +455,8 @@ bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
     p.d = act.d;
     p.n_tok = n_tok;
     p.K = K;
-    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, true>(p, st, grp);
-    else launch_t<T_Q8_0, true>(p, st, grp);
+    if (gate.ty == T_Q4_0) launch_t<T_Q4_0, true>(p, st, grp, nullptr, 0);
+    else launch_t<T_Q8_0, true>(p, st, grp, nullptr, 0);
     return true;
 }
 
