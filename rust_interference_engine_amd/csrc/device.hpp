@@ -232,6 +232,20 @@ __device__ __forceinline__ void wave_sync() {
 // Workgroup barrier for LDS data only: the fences cover the local address space,
 // so it waits for the wave's LDS operations (lgkmcnt) and not for its outstanding
 // global loads, which __syncthreads() (a fence on every address space) waits for.
+// Arrival counts in LDS for a subset of a workgroup's waves (no s_barrier, so
+// waves outside the subset need not get there): lds_arrive publishes the wave's
+// earlier LDS writes (lane 0 adds one), lds_wait_count spins until n arrivals and
+// orders the wave's later LDS reads after them.  The fences cover LDS only, so
+// neither waits for the wave's outstanding global loads.
+__device__ __forceinline__ void lds_arrive(int *cnt) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_wait_count(int *cnt, int n) {
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < n) __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();

@@ -267,6 +267,19 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     // prologue's barriers order LDS only, so the activation is made while the
     // weights are in flight (loads complete in issue order, and a full
     // __syncthreads() would wait for the whole stream).
+    // SPLIT (512 threads): waves 0-3 make the activation before they request any
+    // weights, and meet through LDS arrival counts instead of workgroup barriers;
+    // waves 4-7 request their weights at once and wait for the count.  A wave stalls
+    // on issuing loads while its CU's memory pipeline is full, and everything after
+    // the loads in program order waits with it: with every wave's weight loads
+    // ahead of the prologue, the activation was ready 8 µs (median) into the
+    // gate/up launch, against ~2 µs for the x loads alone.
+    constexpr bool SPLIT = PRO8 && NT == 512;
+    __shared__ int s_arrive;  // SPLIT: arrivals of waves 0-3 (4: norm sums, 8: activation)
+    if constexpr (SPLIT) {
+        if (tid == 0) s_arrive = 0;
+        lds_barrier();  // at entry, before any load
+    }
     float4 xv[4], gv[4];  // values 16τ..16τ+15 of x and of the norm weight
     if constexpr (PRO8) {
 #pragma unroll
@@ -278,7 +291,8 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
                 gv[i] = ((const float4 *)(p.nin.w + 16 * tid))[i];
             }
         }
-        load_pass(base0);  // unconditional (rows are clamped): a group without rows here drops its loads
+        // unconditional (rows are clamped): a group without rows here drops its loads
+        if (!SPLIT || tid >= 256) load_pass(base0);
     }
     constexpr int QG = PROQ ? (QK_PRO_MAX / 16 + NT - 1) / NT : 1;  // PROQ: 16-value groups per thread
     float4 xq[QG][4];  // PROQ: groups τ + NT·g of x
@@ -331,57 +345,70 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
             __shared__ int s_i[128];
             const int K = p.K, nthr = K >> 4;
             const bool act = tid < nthr;
-            float ss = 0.0f;
-            if (act) {
+            if (!SPLIT || tid < 256) {  // SPLIT: waves 0-3 only (wave-uniform)
+                float ss = 0.0f;
+                if (act) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        ss = fmaf(xv[i].x, xv[i].x, ss);
+                        ss = fmaf(xv[i].y, xv[i].y, ss);
+                        ss = fmaf(xv[i].z, xv[i].z, ss);
+                        ss = fmaf(xv[i].w, xv[i].w, ss);
+                    }
+                }
+                ss = wave_sum(ss, 64);
+                if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+                if constexpr (SPLIT) {
+                    lds_arrive(&s_arrive);
+                    lds_wait_count(&s_arrive, 4);
+                } else {
+                    lds_barrier();
+                }
+                const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+                float y[16];
+                float amax = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    ss = fmaf(xv[i].x, xv[i].x, ss);
-                    ss = fmaf(xv[i].y, xv[i].y, ss);
-                    ss = fmaf(xv[i].z, xv[i].z, ss);
-                    ss = fmaf(xv[i].w, xv[i].w, ss);
+                    y[4 * i] = xv[i].x * scale * gv[i].x;
+                    y[4 * i + 1] = xv[i].y * scale * gv[i].y;
+                    y[4 * i + 2] = xv[i].z * scale * gv[i].z;
+                    y[4 * i + 3] = xv[i].w * scale * gv[i].w;
                 }
-            }
-            ss = wave_sum(ss, 64);
-            if ((tid & 63) == 0) s_red[tid >> 6] = ss;
-            lds_barrier();
-            const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
-            float y[16];
-            float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                y[4 * i] = xv[i].x * scale * gv[i].x;
-                y[4 * i + 1] = xv[i].y * scale * gv[i].y;
-                y[4 * i + 2] = xv[i].z * scale * gv[i].z;
-                y[4 * i + 3] = xv[i].w * scale * gv[i].w;
-            }
+                for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(y[i]));
+                amax = fmaxf(amax, xor_f<1>(amax));
+                const float d = amax / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                uint32_t w4[4];
+                int isum = 0;
 #pragma unroll
-            for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(y[i]));
-            amax = fmaxf(amax, xor_f<1>(amax));
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            uint32_t w4[4];
-            int isum = 0;
+                for (int j = 0; j < 4; j++) {
+                    uint32_t v = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    int q = (int)rintf(y[4 * j + e] * id);
-                    q = q < -127 ? -127 : (q > 127 ? 127 : q);
-                    isum += q;
-                    v |= ((uint32_t)(q & 0xff)) << (8 * e);
+                    for (int e = 0; e < 4; e++) {
+                        int q = (int)rintf(y[4 * j + e] * id);
+                        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                        isum += q;
+                        v |= ((uint32_t)(q & 0xff)) << (8 * e);
+                    }
+                    w4[j] = v;
                 }
-                w4[j] = v;
-            }
-            isum += xor_i<1>(isum);
-            if (act) {
-                *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-                if ((tid & 1) == 0) {
-                    s_d[tid >> 1] = d;
-                    s_i[tid >> 1] = isum;
+                isum += xor_i<1>(isum);
+                if (act) {
+                    *(uint4 *)(s_q + 16 * tid) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                    if ((tid & 1) == 0) {
+                        s_d[tid >> 1] = d;
+                        s_i[tid >> 1] = isum;
+                    }
                 }
-            }
-            lds_barrier();
+                if constexpr (SPLIT) {
+                    lds_arrive(&s_arrive);
+                    load_pass(base0);  // waves 0-3 request their weights now
+                } else {
+                    lds_barrier();
+                }
+            }  // prologue waves
+            if constexpr (SPLIT) lds_wait_count(&s_arrive, 8);
 #pragma unroll
             for (int k = 0; k < UPL; k++) {
                 const uint4 *src = (const uint4 *)(s_q + 64 * uu[k]);
