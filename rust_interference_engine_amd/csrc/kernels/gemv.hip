@@ -263,6 +263,16 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
         }
     };
     const int base0 = grp * R;
+    // EPI_ADD over long rows (256 lanes per row, quantized weights, no prologue:
+    // the down projection): the residual value of the first row this thread adds to
+    // in the epilogue (8 threads per row, rows tid/8, tid/8 + NT/8, …) is requested
+    // at entry, so the epilogue's read-modify-write is not one more memory round
+    // trip after the reduction.  A row has one writer in the launch, so the early
+    // value is the one the add uses.  (In the other instances it measured no gain.)
+    constexpr bool EP_PRE = !GLU && !PRO8 && !PROQ && LPR == 256 && TY != T_F32;
+    const int ep_i0 = tid >> 3;
+    const bool ep_pre = EP_PRE && p.seg[sg].epi == EPI_ADD && (tid & 7) == 0 && ep_i0 < p.tr && row0 + ep_i0 < seg_rows;
+    const float ep_res = ep_pre ? p.seg[sg].out[row0 + ep_i0] : 0.0f;
     // PRO8: x and the norm weight are requested before the weight stream, and the
     // prologue's barriers order LDS only, so the activation is made while the
     // weights are in flight (loads complete in issue order, and a full
@@ -614,7 +624,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
             float v = sum;
             if constexpr (GLU) v = (p.glu == 2 ? gelu_tanh_f(sum) : silu_f(sum)) * sum2;
             float *out = p.seg[sg].out;
-            if (p.seg[sg].epi == EPI_ADD) out[r] += v;
+            if (p.seg[sg].epi == EPI_ADD) out[r] = (ep_pre && i == ep_i0 ? ep_res : out[r]) + v;
             else out[r] = v;
             hv[i] = v;
         }
