@@ -172,24 +172,38 @@ int32_t rie_hip_time_ffn_glu(rie_hip_backend *b, int32_t reps, double *avg_us, s
 int32_t rie_hip_k_rmsnorm_quant(const float *x, const float *w, float eps, int32_t n, int32_t k, int32_t fmt, float *xn, int8_t *qs,
                                 float *d, float *s, int32_t *isum, int16_t *bsums);
 /* out[t*rows + r] = W[r] · act[t] for one ggml weight matrix (kernels/mod.rs:136-232).
- * The kernels read whole aligned words around each block, so w must stay readable
- * for 4096 bytes past its last row (the backend's weight upload keeps that slack). */
+ * w may end at its last row: the kernels read whole aligned words around each
+ * block, up to 4 KiB past the matrix, so these entry points run on a padded copy
+ * of w (allocated and freed inside the call). */
 int32_t rie_hip_k_gemv(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, const int8_t *qs, const float *d, const float *s,
                        const int32_t *isum, const int16_t *bsums, const float *act_f32, int32_t n_tok, float *out);
 /* the int8 MFMA prompt GEMM on the same operands (n_tok > 8) */
 int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, const int8_t *qs, const float *d, const float *s,
                        const int32_t *isum, const int16_t *bsums, int32_t n_tok, float *out);
+/* MoE routing of n_tok tokens (moe_ffn's routing, model/cpu.rs:487-501): softmax
+ * over each token's n_exp router logits (ops.rs:38-49), the k most probable
+ * experts with the lower index first on ties (NaN probabilities compare Equal, so
+ * a token whose probabilities are NaN takes experts 0..k-1), weights p/Σ_top p
+ * (norm_topk), p, or 1 (unit_weights).  sel/wgt [n_tok][k] receive each token's
+ * choices in ascending expert order.  1 ≤ k ≤ min(n_exp, 64), n_exp ≤ 512; other
+ * sizes return RIE_HIP_ERR_RUNTIME. */
+int32_t rie_hip_k_moe_route(const float *logits, int32_t n_tok, int32_t n_exp, int32_t k, int32_t norm_topk, int32_t unit_weights,
+                            int32_t *sel, float *wgt);
 /* greedy argmax (sampler.rs:199-209) of n floats */
 int32_t rie_hip_k_argmax(const float *x, int32_t n, uint32_t *out_idx);
 /* The same argmax without allocating device memory.  No counterpart in the
- * reference: for callers that cannot call hipMalloc (code under HIP graph
- * capture, tight serving loops, harnesses that forbid allocation).  The partial
- * maxima live in a fixed 8 KiB array of the library's static device memory (one
- * copy per GPU, held until the process ends), so n must be in 1..1048576
- * (1024 partials of up to 1024 values); larger or empty inputs return
- * RIE_HIP_ERR_RUNTIME with the reason in err.  Calls that overlap on one GPU
- * (from several host threads) share that array and race. */
-int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, char *err, size_t err_len);
+ * reference: for callers that cannot call hipMalloc (code under HIP stream or
+ * graph capture, tight serving loops, harnesses that forbid allocation).  The
+ * partial maxima live in a fixed 8 KiB array of the library's static device
+ * memory (one copy per GPU, held until the process ends), so n must be in
+ * 1..1048576 (1024 partials of up to 1024 values); larger or empty inputs return
+ * RIE_HIP_ERR_RUNTIME with the reason in err.  stream: a hipStream_t to launch on
+ * (the call returns once the two kernels are queued, without synchronizing, so
+ * it can be recorded under capture), or NULL: the null stream, and the call
+ * returns after the result is written.  The first call on a device looks up the
+ * array's address (hipGetSymbolAddress), so make it outside capture.  Calls that
+ * overlap on one GPU (several streams or host threads) share that array and race. */
+int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, void *stream, char *err, size_t err_len);
 
 #ifdef __cplusplus
 }

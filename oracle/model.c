@@ -805,6 +805,61 @@ static void dense_ffn(or_backend *b, const dense_t *d, const float *x, size_t n,
     matmul1(b->pool, &b->acts, &d->down, out);
 }
 
+/* The routing of one token, cpu.rs:492-500: softmax in place (ops.rs:38-49),
+ * sort descending by probability with the comparator
+ * `l[b].partial_cmp(&l[a]).unwrap_or(Equal).then(a.cmp(&b))` (a NaN pair compares
+ * Equal and falls back to the index), then the top k with weights p/norm, where
+ * norm is the sum of the top k in sorted order (norm_topk) or 1, or 1 for unit
+ * weights.  choice/w receive the k experts in sorted order. */
+static void route_token(float *l, size_t ne, size_t k, int norm_topk, int unit_weights, size_t *choice, float *w) {
+    or_softmax(l, ne);
+    size_t *idx = (size_t *)malloc(ne * sizeof(size_t));
+    for (size_t i = 0; i < ne; i++) idx[i] = i;
+    for (size_t i = 1; i < ne; i++) { /* insertion sort: stable, deterministic */
+        size_t cur = idx[i], j = i;
+        while (j > 0) {
+            size_t pv = idx[j - 1];
+            int before;
+            if (l[cur] > l[pv]) before = 1;
+            else if (l[cur] < l[pv]) before = 0;
+            else before = cur < pv; /* Equal, or unordered (NaN) */
+            if (!before) break;
+            idx[j] = pv;
+            j--;
+        }
+        idx[j] = cur;
+    }
+    float norm = 1.0f;
+    if (norm_topk) {
+        norm = 0.0f;
+        for (size_t q = 0; q < k; q++) norm += l[idx[q]];
+    }
+    for (size_t q = 0; q < k; q++) {
+        choice[q] = idx[q];
+        w[q] = unit_weights ? 1.0f : l[idx[q]] / norm;
+    }
+    free(idx);
+}
+
+void or_moe_route(const float *logits, size_t n_tok, size_t n_exp, size_t k, int norm_topk, int unit_weights, int32_t *sel,
+                  float *wgt) {
+    float *l = (float *)malloc(n_exp * sizeof(float));
+    size_t *ch = (size_t *)malloc(k * sizeof(size_t));
+    float *w = (float *)malloc(k * sizeof(float));
+    for (size_t t = 0; t < n_tok; t++) {
+        memcpy(l, logits + t * n_exp, n_exp * sizeof(float));
+        route_token(l, n_exp, k, norm_topk, unit_weights, ch, w);
+        /* ascending expert order: the order in which moe_ffn adds the experts' outputs */
+        for (size_t q = 0; q < k; q++) {
+            size_t rank = 0;
+            for (size_t r = 0; r < k; r++) rank += ch[r] < ch[q];
+            sel[t * k + rank] = (int32_t)ch[q];
+            wgt[t * k + rank] = w[q];
+        }
+    }
+    free(l); free(ch); free(w);
+}
+
 /* cpu.rs:473-524 */
 static void moe_ffn(or_backend *b, const moe_t *mo, const float *x, size_t n, float *out, size_t il) {
     size_t e = mo->router.cols, ne = mo->router.rows;
@@ -817,31 +872,13 @@ static void moe_ffn(or_backend *b, const moe_t *mo, const float *x, size_t n, fl
     size_t *tok = (size_t *)malloc(ne * n * sizeof(size_t));
     float *wgt = (float *)malloc(ne * n * sizeof(float));
     size_t *idx = (size_t *)malloc(ne * sizeof(size_t));
+    float *tw = (float *)malloc(ne * sizeof(float));
     for (size_t t = 0; t < n; t++) {
-        float *l = b->moe_logits + t * ne;
-        or_softmax(l, ne);
-        for (size_t i = 0; i < ne; i++) idx[i] = i;
-        /* sort descending by probability, ties by index (cpu.rs:495) */
-        for (size_t i = 1; i < ne; i++) {
-            size_t cur = idx[i], j = i;
-            while (j > 0) {
-                size_t pv = idx[j - 1];
-                int before = l[cur] > l[pv] || (l[cur] == l[pv] && cur < pv);
-                if (!before) break;
-                idx[j] = pv;
-                j--;
-            }
-            idx[j] = cur;
-        }
-        float norm = 1.0f;
-        if (mo->norm_topk) {
-            norm = 0.0f;
-            for (size_t k = 0; k < mo->n_used; k++) norm += l[idx[k]];
-        }
+        route_token(b->moe_logits + t * ne, ne, mo->n_used, mo->norm_topk, mo->unit_weights, idx, tw);
         for (size_t k = 0; k < mo->n_used; k++) {
             size_t i = idx[k];
             tok[i * n + cnt[i]] = t;
-            wgt[i * n + cnt[i]] = mo->unit_weights ? 1.0f : l[i] / norm;
+            wgt[i * n + cnt[i]] = tw[k];
             cnt[i]++;
         }
     }
@@ -866,7 +903,7 @@ static void moe_ffn(or_backend *b, const moe_t *mo, const float *x, size_t n, fl
             for (size_t i = 0; i < e; i++) out[t * e + i] += scale * b->ys[t * e + i];
         }
     }
-    free(cnt); free(tok); free(wgt); free(idx);
+    free(cnt); free(tok); free(wgt); free(idx); free(tw);
 }
 
 static void residual_add(float *x, const float *y, size_t n, float scale) {

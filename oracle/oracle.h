@@ -97,6 +97,11 @@ void or_rope_inv_freq(size_t dim, float base, float freq_scale, const float *fac
 void or_rope_table(const float *inv_freq, size_t half, size_t pos, float *cos_out, float *sin_out);
 void or_rope_apply(float *x, size_t dim, int neox, const float *cos_t, const float *sin_t);
 
+/* MoE routing of n_tok tokens (model/cpu.rs:492-500): per token the k chosen
+ * experts in ascending expert order (sel) and their weights (wgt), [n_tok][k]. */
+void or_moe_route(const float *logits, size_t n_tok, size_t n_exp, size_t k, int norm_topk, int unit_weights, int32_t *sel,
+                  float *wgt);
+
 /* ---- turbo.rs ----------------------------------------------------------- */
 #define OR_TURBO_KV_SEED 0x75426F5175616E74ULL
 size_t or_turbo_block_size(size_t d);

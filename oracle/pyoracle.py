@@ -82,6 +82,7 @@ def lib():
             "or_hidden": (P, [P, C.POINTER(S)]), "or_kv_layer": (P, [P, S, I, C.POINTER(S)]),
             "or_set_capture": (None, [P, I]), "or_capture": (P, [P, S, I, C.POINTER(S)]),
             "or_argmax": (C.c_uint32, [P, S]),
+            "or_moe_route": (None, [P, S, S, S, I, I, P, P]),
             "or_greedy": (I, [P, P, S, S, S, P, P, P, C.c_char_p, S]),
             "or_bench": (I, [P, S, S, C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_char_p, S]),
         }
@@ -330,3 +331,14 @@ class Backend:
 def argmax(x: np.ndarray) -> int:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return lib().or_argmax(ptr(x), x.size)
+
+
+def moe_route(logits: np.ndarray, k: int, norm_topk: bool = True, unit_weights: bool = False):
+    """moe_ffn's routing (model/cpu.rs:492-500) of logits [n_tok][n_exp]: the k
+    chosen experts per token in ascending expert order, and their weights."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    n_tok, n_exp = logits.shape
+    sel = np.zeros((n_tok, k), np.int32)
+    wgt = np.zeros((n_tok, k), np.float32)
+    lib().or_moe_route(ptr(logits), n_tok, n_exp, k, int(norm_topk), int(unit_weights), ptr(sel), ptr(wgt))
+    return sel, wgt

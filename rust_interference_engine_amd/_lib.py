@@ -73,8 +73,9 @@ def lib():
         "rie_hip_k_rmsnorm_quant": (I, [P, P, F, I, I, I, P, P, P, P, P, P]),
         "rie_hip_k_gemv": (I, [I, P, I, I, P, P, P, P, P, P, I, P]),
         "rie_hip_k_gemm": (I, [I, P, I, I, P, P, P, P, P, I, P]),
+        "rie_hip_k_moe_route": (I, [P, I, I, I, I, I, P, P]),
         "rie_hip_k_argmax": (I, [P, I, P]),
-        "rie_hip_k_argmax_noalloc": (I, [P, I, P, CP, S]),
+        "rie_hip_k_argmax_noalloc": (I, [P, I, P, P, CP, S]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

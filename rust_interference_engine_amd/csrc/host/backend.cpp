@@ -830,10 +830,14 @@ void HipBackend::decode_step_graph(size_t pos) {
         }
         RIE_HIP_CHECK(hipStreamEndCapture(st_, &dg.graph));
         in_capture_ = false;
+        dg.head_normed = head_normed_;
+        dg.head_first = head_first_;
         RIE_HIP_CHECK(hipGraphInstantiate(&dg.exec, dg.graph, nullptr, nullptr, 0));
         it = graphs_.emplace(ns, dg).first;
     }
     RIE_HIP_CHECK(hipGraphLaunch(it->second.exec, st_));
+    head_normed_ = it->second.head_normed;
+    head_first_ = it->second.head_first;
 }
 
 // One greedy step as a graph (per attention range count): run_layers at the
@@ -858,10 +862,14 @@ void HipBackend::greedy_step_graph(size_t pos) {
         }
         RIE_HIP_CHECK(hipStreamEndCapture(st_, &dg.graph));
         in_capture_ = false;
+        dg.head_normed = head_normed_;
+        dg.head_first = head_first_;
         RIE_HIP_CHECK(hipGraphInstantiate(&dg.exec, dg.graph, nullptr, nullptr, 0));
         it = greedy_graphs_.emplace(ns, dg).first;
     }
     RIE_HIP_CHECK(hipGraphLaunch(it->second.exec, st_));
+    head_normed_ = it->second.head_normed;
+    head_first_ = it->second.head_first;
 }
 
 int HipBackend::splits_for(size_t n, size_t pos) const {

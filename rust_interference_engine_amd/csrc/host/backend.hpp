@@ -164,6 +164,10 @@ class HipBackend {
     struct DecodeGraph {
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
+        // the head's state as captured: every replay leaves d_x_/d_xn_ as the
+        // captured launches do, so Backend::hidden must see these values again
+        bool head_normed = true;
+        int head_first = 0;
     };
     std::map<int, DecodeGraph> graphs_;  // by attention range count
     std::map<int, DecodeGraph> greedy_graphs_;  // the same with the advancing argmax (generate_greedy)

@@ -251,6 +251,26 @@ static rie::DevWeight mkw(int32_t ty, const uint8_t *w, int32_t rows, int32_t k)
     return dw;
 }
 
+// The kernels read whole aligned words around each block, up to 4 KiB past a
+// matrix's last row (the backend's weight upload carries that slack).  A caller's
+// buffer may end at the last row, so the kernel entry points run on a copy with
+// the slack; the copy is freed when the call returns.
+struct PaddedWeight {
+    uint8_t *data = nullptr;
+    PaddedWeight(int32_t ty, const uint8_t *w, int32_t rows, int32_t k) {
+        if (!w || rows < 1 || k < 1 || !rie::block_bytes(ty) || k % (int32_t)rie::block_size(ty)) throw Error{rie::E_UNSUPPORTED, "unsupported weight type/shape"};
+        const size_t bytes = (size_t)rows * rie::row_bytes(ty, (size_t)k);
+        RIE_HIP_CHECK(hipMalloc(&data, bytes + 4096));
+        RIE_HIP_CHECK(hipMemset(data + bytes, 0, 4096));
+        RIE_HIP_CHECK(hipMemcpy(data, w, bytes, hipMemcpyDeviceToDevice));
+    }
+    ~PaddedWeight() {
+        if (data) (void)hipFree(data);
+    }
+    PaddedWeight(const PaddedWeight &) = delete;
+    PaddedWeight &operator=(const PaddedWeight &) = delete;
+};
+
 int32_t rie_hip_k_gemv(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, const int8_t *qs, const float *d, const float *s,
                        const int32_t *isum, const int16_t *bsums, const float *act_f32, int32_t n_tok, float *out) {
     return guarded(nullptr, 0, [&] {
@@ -260,7 +280,8 @@ int32_t rie_hip_k_gemv(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
         a.s = const_cast<float *>(s);
         a.isum = const_cast<int32_t *>(isum);
         a.bsums = const_cast<int16_t *>(bsums);
-        rie::GemvSeg sg{mkw(ty, w, rows, k), out, rows, rie::EPI_STORE};
+        PaddedWeight pw(ty, w, rows, k);
+        rie::GemvSeg sg{mkw(ty, pw.data, rows, k), out, rows, rie::EPI_STORE};
         if (!rie::launch_gemv(&sg, 1, a, act_f32, n_tok, k, 0)) throw Error{rie::E_UNSUPPORTED, "unsupported weight type/shape"};
         RIE_HIP_CHECK(hipGetLastError());
         RIE_HIP_CHECK(hipDeviceSynchronize());
@@ -276,9 +297,13 @@ int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
         a.s = const_cast<float *>(s);
         a.isum = const_cast<int32_t *>(isum);
         a.bsums = const_cast<int16_t *>(bsums);
-        rie::GemvSeg sg{mkw(ty, w, rows, k), out, rows, rie::EPI_STORE};
-        // room for the partial sums of a K split (three planes), as the backend has
-        const size_t cap = 3 * (size_t)std::max(n_tok, 0) * (size_t)std::max(rows, 0);
+        PaddedWeight pw(ty, w, rows, k);
+        rie::GemvSeg sg{mkw(ty, pw.data, rows, k), out, rows, rie::EPI_STORE};
+        // room for the partial sums of a K split (up to three planes, capped at
+        // 64 MiB like the backend's workspace), only where a split can happen:
+        // Q4_0/Q8_0 weights, over 64 tokens and at least 64 stages of 128 values
+        const bool can_split = (ty == rie::T_Q4_0 || ty == rie::T_Q8_0) && n_tok > 64 && k / 128 >= 64;
+        const size_t cap = can_split ? std::min<size_t>(3 * (size_t)n_tok * (size_t)std::max(rows, 0), (size_t)1 << 24) : 0;
         float *part = nullptr;
         if (cap) RIE_HIP_CHECK(hipMalloc(&part, cap * sizeof(float)));
         const bool ok = rie::gemm_supported(ty, (size_t)k) && rie::launch_gemm(&sg, 1, a, n_tok, k, 0, nullptr, part, cap);
@@ -288,6 +313,17 @@ int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
         if (!ok) throw Error{rie::E_UNSUPPORTED, "no GEMM kernel for this weight type/shape"};
         RIE_HIP_CHECK(e);
         RIE_HIP_CHECK(e2);
+    });
+}
+
+int32_t rie_hip_k_moe_route(const float *logits, int32_t n_tok, int32_t n_exp, int32_t k, int32_t norm_topk, int32_t unit_weights,
+                            int32_t *sel, float *wgt) {
+    return guarded(nullptr, 0, [&] {
+        if (n_tok < 1 || n_exp < 1 || n_exp > 512 || k < 1 || k > n_exp || k > 64 || !logits || !sel || !wgt)
+            throw Error{rie::E_RUNTIME, "bad routing sizes"};
+        rie::launch_moe_route(logits, n_tok, n_exp, k, norm_topk, unit_weights, sel, wgt, 0);
+        RIE_HIP_CHECK(hipGetLastError());
+        RIE_HIP_CHECK(hipDeviceSynchronize());
     });
 }
 
@@ -307,11 +343,11 @@ int32_t rie_hip_k_argmax(const float *x, int32_t n, uint32_t *out_idx) {
     });
 }
 
-int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, char *err, size_t err_len) {
+int32_t rie_hip_k_argmax_noalloc(const float *x, int32_t n, uint32_t *out_idx, void *stream, char *err, size_t err_len) {
     return guarded(err, err_len, [&] {
-        rie::launch_argmax_noalloc(x, n, out_idx, 0);
+        rie::launch_argmax_noalloc(x, n, out_idx, (hipStream_t)stream);
         RIE_HIP_CHECK(hipGetLastError());
-        RIE_HIP_CHECK(hipDeviceSynchronize());
+        if (!stream) RIE_HIP_CHECK(hipDeviceSynchronize());
     });
 }
 

@@ -68,6 +68,7 @@ struct DecP {
     // rows [j·slot_rows, (j+1)·slot_rows) of the launch are rows of expert xsel[j]
     const int *xsel;
     int slot_rows;
+    int n_xsel;        // experts in the stacked matrices: a selection is clamped below it
     int act_per_slot;  // slot j reads activation row j (the down projection of expert j's hidden)
     RouteEpi route;    // F32 router of one token: the last workgroup routes it (route.cnt != nullptr)
 };
@@ -243,9 +244,12 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     int slot = 0;
     if (p.xsel) {  // a workgroup's rows lie in one slot (slot_rows is a multiple of the tile)
         slot = row0 / p.slot_rows;
-        const size_t off = ((size_t)p.xsel[slot] - (size_t)slot) * (size_t)p.slot_rows * rb;
+        // the routing writes every selection below the expert count; the clamp keeps
+        // the weight stream inside the stacked matrices whatever the ids hold
+        const int e = min((unsigned)p.xsel[slot], (unsigned)(p.n_xsel - 1));
+        const size_t off = ((size_t)e - (size_t)slot) * (size_t)p.slot_rows * rb;
         wbase += off;
-        if constexpr (GLU) wbase2 += ((size_t)p.xsel[slot] - (size_t)slot) * (size_t)p.slot_rows * p.seg[1].rb;
+        if constexpr (GLU) wbase2 += ((size_t)e - (size_t)slot) * (size_t)p.slot_rows * p.seg[1].rb;
     }
     Raw<TY> raw[NW][R][UPL];
     auto load_pass = [&](int base) {
@@ -1013,6 +1017,7 @@ bool launch_gemv_experts(const DevWeight &stacked, int slot_rows, const int *sel
     d.actf = act_f32;
     d.xsel = sel;
     d.slot_rows = slot_rows;
+    d.n_xsel = (int)(stacked.rows / (size_t)slot_rows);
     d.act_per_slot = act_per_slot;
     if (nin) d.nin = *nin;
     return dispatch_dec(stacked.ty, d, st);
@@ -1038,6 +1043,7 @@ bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff,
     if (nin) d.nin = *nin;
     d.xsel = sel;
     d.slot_rows = ff;
+    d.n_xsel = (int)(gate.rows / (size_t)ff);
     return dispatch_dec(gate.ty, d, st);
 }
 

@@ -61,13 +61,30 @@ __device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int 
             if (lane + 64 * i < n_exp && !((taken >> i) & 1u)) v = fmaxf(v, pr[i]);
         v = row_max16(v);
         const auto rl = [&](int ln) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), ln)); };
-        const float m = fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));  // the row maxima
+        float m = fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));  // the row maxima
         int idx = 0x7fffffff;
 #pragma unroll
         for (int i = NE - 1; i >= 0; i--) {  // the lowest expert index holding m
             const bool cand = lane + 64 * i < n_exp && !((taken >> i) & 1u) && pr[i] == m;
             const uint64_t b = __ballot(cand);
             if (b) idx = 64 * i + __builtin_ctzll(b);
+        }
+        if (idx == 0x7fffffff) {
+            // No expert left holds a number: the probabilities are NaN (a NaN or
+            // +Inf logit, or every logit -Inf, makes the softmax sum NaN).  The
+            // reference's comparator calls NaN pairs Equal and falls back to the
+            // index (cpu.rs:495), so the lowest untaken expert comes next, with
+            // its NaN probability.
+#pragma unroll
+            for (int i = NE - 1; i >= 0; i--) {
+                const uint64_t b = __ballot(lane + 64 * i < n_exp && !((taken >> i) & 1u));
+                if (b) idx = 64 * i + __builtin_ctzll(b);
+            }
+            float pv = pr[0];
+#pragma unroll
+            for (int i = 1; i < NE; i++)
+                if ((idx >> 6) == i) pv = pr[i];
+            m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), idx & 63));
         }
         if (idx < n_exp && (idx & 63) == lane) taken |= 1u << (idx >> 6);
         if (lane == j) {

@@ -134,8 +134,8 @@ def test_rmsnorm_then_quant_bitwise(oracle, cuda, k):
 
 def _gemv(ty, w, rows, k, act, act_f32, n_tok, cuda, gemm=False):
     L = R.lib()
-    # the weight buffer keeps the library's 4096 readable bytes past the last row
-    wd = dev(np.concatenate([w, np.zeros(4096, np.uint8)]), cuda)
+    # an exact-size buffer: the entry points pad a copy for the kernels' word reads
+    wd = dev(np.ascontiguousarray(w, dtype=np.uint8), cuda)
     out = torch.zeros(n_tok * rows, dtype=torch.float32, device=cuda)
     qs, d, s, isum, bs = act if act is not None else (None,) * 5
     p = lambda t: t.data_ptr() if t is not None else None
@@ -257,6 +257,41 @@ def test_argmax_first_index(oracle, cuda):
         out = torch.zeros(1, dtype=torch.int32, device=cuda)
         assert L.rie_hip_k_argmax(xd.data_ptr(), n, out.data_ptr()) == 0
         assert int(host(out)[0]) == oracle.argmax(x) == n // 3
+
+
+def test_moe_routing_matches_oracle_with_nonfinite_logits(oracle, cuda):
+    """The routing wave (softmax, top-k with the index tie-break, weights) against
+    the oracle's routing (model/cpu.rs:492-500), including rows whose softmax is NaN
+    (a NaN or +Inf logit, or every logit -Inf): the reference's comparator calls
+    NaN pairs Equal and takes experts 0..k-1.  Every selection must name a real
+    expert, since the expert GEMVs address their weights with it."""
+    L = R.lib()
+    rng = np.random.default_rng(5)
+    for n_exp, k in ((8, 2), (60, 4), (64, 6), (128, 8), (256, 8), (512, 16)):
+        n_tok = 48
+        logits = (rng.integers(-6, 7, size=(n_tok, n_exp)) * 0.5).astype(np.float32)  # exact ties
+        logits[1::4] = rng.standard_normal((len(logits[1::4]), n_exp)).astype(np.float32)
+        logits[2, 5 % n_exp] = np.nan
+        logits[3, n_exp - 1] = np.inf
+        logits[5, :] = -np.inf
+        logits[6, : n_exp // 2] = -np.inf
+        logits[7, 0] = -np.inf
+        logits[9, :] = np.nan
+        for norm_topk, unit in ((1, 0), (0, 0), (1, 1)):
+            want_s, want_w = oracle.moe_route(logits, k, bool(norm_topk), bool(unit))
+            ld = dev(logits, cuda)
+            sel = torch.full((n_tok * k,), -7, dtype=torch.int32, device=cuda)
+            wgt = torch.zeros(n_tok * k, dtype=torch.float32, device=cuda)
+            assert L.rie_hip_k_moe_route(ld.data_ptr(), n_tok, n_exp, k, norm_topk, unit, sel.data_ptr(), wgt.data_ptr()) == 0
+            got_s = host(sel).reshape(n_tok, k)
+            got_w = host(wgt).reshape(n_tok, k)
+            assert ((got_s >= 0) & (got_s < n_exp)).all()
+            assert np.array_equal(got_s, want_s), (n_exp, k, np.argwhere(got_s != want_s)[:4])
+            assert np.array_equal(np.isnan(got_w), np.isnan(want_w))
+            fin = ~np.isnan(want_w)
+            np.testing.assert_allclose(got_w[fin], want_w[fin], rtol=4e-6, atol=1e-8)
+            for t in (2, 3, 5, 9):  # NaN softmax: the first k experts
+                assert got_s[t].tolist() == list(range(k))
 
 
 # ---- whole model ------------------------------------------------------------------------------
@@ -779,6 +814,39 @@ def test_hidden_and_error_contract(oracle, cuda):
         assert ei.value.kind == "Runtime"
     with pytest.raises(R.RieError, match="logits buffer too small"):
         g.forward([1, 2], 0, logits=np.zeros(10, np.float32))
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q4_K])
+def test_hidden_after_graph_replayed_decode_steps(cuda, ty):
+    """Backend::hidden (model/mod.rs:314-319; read every decode step by the
+    adapter path, engine.rs:304-320, 442) after single-token forwards that replay
+    a captured graph: each call must return that step's normalized row, bitwise
+    the row an eager backend (no graph) forms for the same tokens."""
+    spec = synth.tiny("llama", ty)
+    img = synth.build(spec)
+    g = R.HipBackend(img, n_ctx=64, max_batch=4)
+    e = R.HipBackend(img, n_ctx=64, max_batch=4, use_graph=False)
+    prompt = [3, 14, 15, 92]
+    g.forward(prompt, 0)
+    e.forward(prompt, 0)
+    assert np.array_equal(g.hidden(), e.hidden())
+    tok, rows = 7, []
+    for step in range(6):  # step 0 captures the graph, the rest replay it
+        lg = g.forward([tok], 4 + step)
+        le = e.forward([tok], 4 + step)
+        assert np.array_equal(lg, le)
+        hg, he = g.hidden(), e.hidden()
+        assert np.array_equal(hg, he), step
+        assert np.array_equal(g.hidden(), hg)  # asking twice gives the same row
+        rows.append(hg)
+        tok = int(np.argmax(lg))
+    assert not any(np.array_equal(rows[i], rows[i + 1]) for i in range(len(rows) - 1))
+    # the on-device greedy loop (one graph per step) leaves its last step's row
+    nxt = g.forward_argmax([tok], 10)
+    assert nxt == e.forward_argmax([tok], 10)
+    g.generate_greedy(11, 3)
+    e.generate_greedy(11, 3)
+    assert np.array_equal(g.hidden(), e.hidden())
 
 
 def test_engine_prefix_reuse(oracle, cuda):

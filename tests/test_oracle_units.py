@@ -538,3 +538,53 @@ def test_quantize_weights_roundtrip(oracle):
     for ty, tol in ((8, 0.01), (2, 0.15)):
         y = G.dequantize(ty, oracle.quantize_weights(ty, x), 1024)
         assert np.abs(y - x).max() <= tol * np.abs(x).max()
+
+
+# ---- MoE routing (model/cpu.rs:492-500) ---------------------------------------------------------
+def _route_numpy(logits, k, norm_topk=True, unit_weights=False):
+    """Independent restatement: f64 softmax, then a stable sort on (-p, index)."""
+    sel, wgt = [], []
+    for row in logits.astype(np.float64):
+        p = np.exp(row - row.max())
+        p /= p.sum()
+        order = np.lexsort((np.arange(p.size), -p))[:k]
+        w = np.ones(k) if unit_weights else (p[order] / p[order].sum() if norm_topk else p[order])
+        asc = np.argsort(order)
+        sel.append(order[asc])
+        wgt.append(w[asc])
+    return np.array(sel, np.int32), np.array(wgt)
+
+
+def test_moe_route_known_answers(oracle):
+    nan, inf = np.nan, np.inf
+    # equal top pair: index order, weights exactly 1/2
+    s, w = oracle.moe_route(np.array([[0, 2, 2, 1]], np.float32), 2)
+    assert s.tolist() == [[1, 2]] and w.tolist() == [[0.5, 0.5]]
+    # a three-way tie keeps the two lowest indices
+    s, _ = oracle.moe_route(np.array([[1, 1, 1, 0]], np.float32), 2)
+    assert s.tolist() == [[0, 1]]
+    # -Inf logits get probability 0; the zero tie is broken by index
+    s, w = oracle.moe_route(np.array([[-inf, 0, -inf, 0]], np.float32), 3)
+    assert s.tolist() == [[0, 1, 3]] and w.tolist() == [[0.0, 0.5, 0.5]]
+    # NaN, +Inf, or every logit -Inf: the softmax is NaN everywhere, every pair
+    # compares Equal, so the first k experts are taken, with NaN weights
+    for row in ([0, nan, 3, 1], [0, inf, 3, 1], [-inf] * 4):
+        s, w = oracle.moe_route(np.array([row], np.float32), 2)
+        assert s.tolist() == [[0, 1]] and np.isnan(w).all()
+        s, w = oracle.moe_route(np.array([row], np.float32), 2, unit_weights=True)
+        assert s.tolist() == [[0, 1]] and w.tolist() == [[1.0, 1.0]]
+    # without renormalization the weights are the probabilities: e/(e+1+...) closed form
+    s, w = oracle.moe_route(np.array([[1, 0]], np.float32), 1, norm_topk=False)
+    assert s.tolist() == [[0]] and abs(w[0, 0] - np.e / (np.e + 1)) < 1e-6
+
+
+def test_moe_route_matches_numpy_restatement(oracle):
+    rng = np.random.default_rng(11)
+    for n_exp, k in ((8, 2), (64, 6), (128, 8), (60, 4)):
+        logits = (rng.integers(-6, 7, size=(40, n_exp)) * 0.5).astype(np.float32)  # many exact ties
+        logits[::3] = rng.standard_normal((len(logits[::3]), n_exp)).astype(np.float32)
+        for norm_topk, unit in ((True, False), (False, False), (True, True)):
+            s, w = oracle.moe_route(logits, k, norm_topk, unit)
+            s2, w2 = _route_numpy(logits, k, norm_topk, unit)
+            assert np.array_equal(s, s2)
+            np.testing.assert_allclose(w, w2, rtol=2e-6, atol=1e-7)
