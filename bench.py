@@ -1,25 +1,33 @@
 #!/usr/bin/env python3
 """Throughput of RIE's per-token forward loop on one MI355X.
 
-Workload (Llama-3.1-8B-shaped synthetic model, Q4_0): 32 layers, hidden 4096,
-32 query / 8 KV heads of 128, SwiGLU FFN 14336, vocab 128256, untied Q4_0 output
-head, weights N(0, 0.02) quantized with quantize::q4_0, unit norms, RoPE base
-5e5, f16 KV cache.  One step = Engine::bench (crates/rie-core/src/engine.rs:
+Headline workload (Llama-3.1-8B-shaped synthetic model, Q4_0): 32 layers, hidden
+4096, 32 query / 8 KV heads of 128, SwiGLU FFN 14336, vocab 128256, untied Q4_0
+output head, weights N(0, 0.02) quantized with quantize::q4_0, unit norms, RoPE
+base 5e5, f16 KV cache.  One step = Engine::bench (crates/rie-core/src/engine.rs:
 540-564): a 512-token prompt evaluated as one batch (pp512), then 128 greedy
 decode steps (tg128) with on-device argmax.  The GGUF image is uploaded once and
 is resident in HBM before timing starts.
 
-value = tg128 tokens/s; pp512 tokens/s is reported beside it, with its int8
-MFMA roofline (2·tokens·layer parameters, the head for the last token, over 5
-POPS).  The roofline entry is the dominant decode kernel (the fused
-gate/up/SwiGLU GEMV), timed with HIP events on the backend's stream.
-cpu_baseline is RIE's CPU path restated in C (the oracle) on the same image, on a
-bounded sample, at 8 threads and at every physical core.  --workload selects the
-other benchmark shapes (Qwen3-1.7B Q4_0, Llama-3.2-3B Q4_K_M, Qwen3-30B-A3B Q4_K).
+value = tg128 tokens/s of the headline; pp512 tokens/s is reported beside it,
+with its int8 MFMA roofline (2·tokens·layer parameters, the head for the last
+token, over 5 POPS).  The roofline entry is the dominant decode kernel (the
+fused gate/up/SwiGLU GEMV), timed with HIP events on the backend's stream.
+
+"configs" times the other benchmark workloads in the same run, each one
+warm-up step and one timed step of its own: the Qwen3-1.7B (Q4_0, tied Q6_K
+head), Llama-3.2-3B (Q4_K_M mix) and Qwen3-30B-A3B (MoE, Q4_K) shapes at
+pp512 + tg128, and the 32K-context workload (the 8B model, a 32768-token prompt
+in 512-token batches, then tg128) with Turbo4 and with f16 KV caches.  Each
+carries its decode bytes per token and fraction of the HBM roofline.
+
+cpu_baseline is RIE's CPU path restated in C (the oracle) on the headline image,
+on a bounded sample, at 8 threads and at every physical core.
 """
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -27,17 +35,21 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 WORKLOADS = {
-    # name: (spec builder, description, attention heads (query, kv))
+    # name: (spec builder, description)
     "llama3.1-8b-q4_0": ("baseline_llama31_8b_q4_0", "llama-3.1-8b-shaped q4_0, pp512 then greedy tg128, f16 KV"),
     "qwen3-1.7b-q4_0": ("baseline_qwen3_1_7b_q4_0", "qwen3-1.7b-shaped q4_0 (tied q6_k head), pp512 then greedy tg128, f16 KV"),
     "llama3.2-3b-q4_k_m": ("baseline_llama32_3b_q4_k_m", "llama-3.2-3b-shaped q4_k_m mix (tied q6_k head), pp512 then greedy tg128, f16 KV"),
     "qwen3-30b-a3b-q4_k": ("baseline_qwen3_30b_a3b_q4_k", "qwen3-30b-a3b-shaped moe q4_k (128 experts, top-8), pp512 then greedy tg128, f16 KV"),
 }
 DEFAULT_WORKLOAD = "llama3.1-8b-q4_0"
-INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+OTHER_WORKLOADS = ["qwen3-1.7b-q4_0", "llama3.2-3b-q4_k_m", "qwen3-30b-a3b-q4_k"]
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
 
 
 def main():
@@ -48,12 +60,14 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--gen", type=int, default=128)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default=DEFAULT_WORKLOAD,
-                    help="the benchmark workload (default: the Llama-3.1-8B Q4_0 headline)")
+                    help="the workload of the bench line (default: the Llama-3.1-8B Q4_0 headline)")
+    ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="short run of the roofline kernel (for counters)")
     ap.add_argument("--prefill-only", action="store_true", help="short run of pp512 prompts only (for counters)")
+    ap.add_argument("--decode-only", action="store_true", help="short run of greedy decode steps only (for traces)")
     ap.add_argument("--long-context", action="store_true",
-                    help="the 32K-context workload instead: pp32768 then tg128 on the same 8B Q4_0 model, Turbo4 and f16 KV")
+                    help="only the 32K-context workload: pp32768 then tg128 on the 8B Q4_0 model, Turbo4 and f16 KV")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the forward loop on one GPU; runs on more than one GPU are not part of this build",
@@ -63,14 +77,75 @@ def main():
     if args.kernel_only:
         return kernel_only(args)
     if args.long_context:
-        return long_context(args)
+        print(json.dumps({"metric": "pp32768 and tg128 tok/s at 32K context (Llama-3.1-8B Q4_0; Turbo4 vs f16 KV)",
+                          "n_gpus": 1, **long_context()}), flush=True)
+        return
+    import torch
+
+    assert torch.cuda.is_available(), "needs the MI355X"
+    headline = args.workload == DEFAULT_WORKLOAD
+    if args.prefill_only or args.decode_only:
+        return short_run(args)
+    res, extra, img = measure_workload(args.workload, args.prompt, args.gen, args.steps, args.warmup, full=True)
+
+    out = {
+        "metric": "tg128 tok/s (Llama-3.1-8B Q4_0, after pp512)" if headline else f"tg128 tok/s ({args.workload}, after pp512)",
+        "value": res["tg128_tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x ggml blocks (int32 block dots, f32 accumulate)",
+        "data": "synthetic: N(0,0.02) weights quantized to the workload's ggml types, prompt ids (i*7919+13) mod V",
+        "config": res["config"],
+        "pp512_tok_s": res["pp512_tok_s"],
+        "prefill_tok_s_by_batch": extra["prefill_tok_s_by_batch"],
+        "prefill_roofline": res["prefill_roofline"],
+        "decode_ms_per_token": res["decode_ms_per_token"],
+        "decode_bytes_per_token": res["decode_bytes_per_token"],
+        "decode_effective_gbs": res["decode_effective_gbs"],
+        "decode_frac_hbm_roofline": res["decode_frac_hbm_roofline"],
+        "roofline": extra["roofline"],
+        "eager_decode_kernel_ms": extra["eager_decode_kernel_ms"],
+        "eager_decode_step_ms": extra["eager_decode_step_ms"],
+        "setup_s": res["setup_s"],
+        "greedy_head": res["greedy_head"],
+    }
+    if headline and not args.headline_only:
+        configs = {}
+        for wl in OTHER_WORKLOADS:
+            log(f"config {wl}")
+            configs[wl] = measure_workload(wl, 512, 128, 1, 1, full=False)[0]
+        log("config long-context")
+        configs["llama3.1-8b-q4_0-32k"] = long_context()
+        out["configs"] = configs
+    if not args.no_cpu_baseline and headline:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(img, out["config"]["vocab"])
+    print(json.dumps(out), flush=True)
+
+
+def decode_bytes(costs, n_layer, kv_row_bytes_per_pos, ctx):
+    """Algorithmic bytes of one decode token: every layer matrix once at its stored
+    size (routed experts: the used share), the head, one embedding row, and the
+    K/V rows of ctx cached positions."""
+    return costs["layer_weight_bytes"] + costs["head_bytes"] + costs["embd_row_bytes"] + n_layer * kv_row_bytes_per_pos * ctx
+
+
+def measure_workload(name, n_prompt, n_gen, steps, warmup, full):
+    """pp{n_prompt} as one batch then greedy tg{n_gen}, `steps` timed steps after
+    `warmup` untimed ones.  full: also the prefill-by-batch legs, the roofline
+    kernel timing and the eager per-kernel profile."""
     import torch
 
     import rust_interference_engine_amd as R
     from rust_interference_engine_amd import gguf, synth
 
-    assert torch.cuda.is_available(), "needs the MI355X"
-    builder, wl_desc = WORKLOADS[args.workload]
+    builder, wl_desc = WORKLOADS[name]
     t0 = time.time()
     spec = getattr(synth, builder)(seed=1, ctx=8192)
     img = synth.build_array(spec)
@@ -78,19 +153,10 @@ def main():
     E, V, L = spec.n_embd, spec.n_vocab, spec.n_layer
     kvd = spec.n_head_kv * spec.head_dim
     costs = gguf.per_token_costs(img, spec.n_expert_used if spec.n_expert else 0)
-    n_ctx = args.prompt + args.gen + 64
     t0 = time.time()
-    be = R.HipBackend(img, n_ctx=n_ctx, max_batch=args.prompt, kv_type=R.KvType.F16)
+    be = R.HipBackend(img, n_ctx=n_prompt + n_gen + 64, max_batch=n_prompt, kv_type=R.KvType.F16)
     t_load = time.time() - t0
-    prompt = [(i * 7919 + 13) % V for i in range(args.prompt)]
-
-    if args.prefill_only:  # counter runs: prompts only
-        be.forward_argmax(prompt[:8], 0)
-        for _ in range(max(args.steps, 1)):
-            be.forward_argmax(prompt, 0)
-        torch.cuda.synchronize()
-        print(json.dumps({"prefill_only": args.workload, "steps": args.steps}), flush=True)
-        return
+    prompt = [(i * 7919 + 13) % V for i in range(n_prompt)]
 
     def step():
         torch.cuda.synchronize()
@@ -98,97 +164,150 @@ def main():
         be.forward_argmax(prompt, 0)
         torch.cuda.synchronize()
         b = time.perf_counter()
-        toks = be.generate_greedy(args.prompt, args.gen)
+        toks = be.generate_greedy(n_prompt, n_gen)
         torch.cuda.synchronize()
         c = time.perf_counter()
         return b - a, c - b, toks
 
     be.forward_argmax(prompt[:8], 0)  # Engine::bench warm-up on the first 8 tokens
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     pp_t = tg_t = 0.0
     toks = None
-    for _ in range(args.steps):
+    for _ in range(steps):
         a, b, toks = step()
         pp_t += a
         tg_t += b
     torch.cuda.synchronize()
     total = time.perf_counter() - t_start
-    tg_tps = args.gen * args.steps / tg_t
-    pp_tps = args.prompt * args.steps / pp_t
-
-    # ---- the same 512-token prefill fed in micro-batches of 1, 128 and 512 tokens ----
-    def prefill_batched(b):
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for p0 in range(0, args.prompt, b):
-            be.forward_argmax(prompt[p0:p0 + b], p0)
-        torch.cuda.synchronize()
-        return args.prompt / (time.perf_counter() - t)
-    by_batch = {str(b): round(prefill_batched(b), 1) for b in (1, 128)}
-    by_batch[str(args.prompt)] = round(pp_tps, 1)
-
-    # ---- algorithmic costs: decode bytes per token at mid context, prefill int8 ops ----
-    ctx_mid = args.prompt + args.gen // 2
-    kv_bytes = L * 2 * kvd * 2 * (ctx_mid + 1)  # K and V rows read, f16
-    tok_bytes = costs["layer_weight_bytes"] + costs["head_bytes"] + costs["embd_row_bytes"] + kv_bytes
-    pp_ops = 2 * args.prompt * costs["layer_params"] + 2 * costs["head_params"]  # head for the last token only
-    pp_tops = pp_ops / (pp_t / args.steps) / 1e12
-
-    # ---- roofline of the dominant decode kernel, timed live with HIP events ----
-    # (the single-token gate/up/SwiGLU launch over every layer's weights in turn,
-    # on the backend's stream, so each launch streams its weights from HBM)
-    roofline = None
-    if not spec.n_expert:
-        glu_us, glu_bytes = be.time_ffn_glu(reps=3)
-        achieved = glu_bytes / (glu_us / 1e6) / 1e9
-        roofline = {"bound": "hbm", "kernel": "gemv_dec_kernel gate+up+SwiGLU (RMSNorm+quantization of x in the prologue, "
-                                              "quantized hidden out)",
-                    "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic() if args.workload == DEFAULT_WORKLOAD else None,
-                    "traffic_source": ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel, scaled by a 256 MiB copy: "
-                                       "profiles/gemv_dec_gate_up_glu_llama8b_q4_0_pmc.md (not measured in this run)")
-                    if args.workload == DEFAULT_WORKLOAD else None,
-                    "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_us, 2)}
-    prof = be.profile_decode(ctx_mid, reps=5)
-    step_ms = sum(v[0] for v in prof.values()) / 5
-
-    headline = args.workload == DEFAULT_WORKLOAD
-    out = {
-        "metric": "tg128 tok/s (Llama-3.1-8B Q4_0, after pp512)" if headline else f"tg128 tok/s ({args.workload}, after pp512)",
-        "value": round(tg_tps, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(total / args.steps * 1e3, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8 x ggml blocks (int32 block dots, f32 accumulate)",
-        "data": "synthetic: N(0,0.02) weights quantized to the workload's ggml types, prompt ids (i*7919+13) mod V",
-        "config": {"workload": wl_desc, "prompt": args.prompt, "gen": args.gen, "layers": L, "hidden": E,
+    tg_tps = n_gen * steps / tg_t
+    pp_tps = n_prompt * steps / pp_t
+    ctx_mid = n_prompt + n_gen // 2
+    tok_bytes = decode_bytes(costs, L, 2 * kvd * 2, ctx_mid + 1)  # K and V rows, f16
+    pp_ops = 2 * n_prompt * costs["layer_params"] + 2 * costs["head_params"]  # head for the last token only
+    pp_tops = pp_ops / (pp_t / steps) / 1e12
+    tok_s = tg_t / (n_gen * steps)
+    res = {
+        "config": {"workload": wl_desc, "prompt": n_prompt, "gen": n_gen, "layers": L, "hidden": E,
                    "ffn": spec.n_ff_exp if spec.n_expert else spec.n_ff, "vocab": V, "heads": [spec.n_head, spec.n_head_kv],
                    "experts": [spec.n_expert, spec.n_expert_used] if spec.n_expert else None},
+        "tg128_tok_s": round(tg_tps, 2),
         "pp512_tok_s": round(pp_tps, 1),
-        "prefill_tok_s_by_batch": by_batch,
+        "ms_per_step": round(total / steps * 1e3, 3),
+        "steps": steps,
         "prefill_roofline": {"bound": "mfma", "achieved": round(pp_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
                              "frac": round(pp_tops / INT8_PEAK_TOPS, 4), "ops_per_prompt": int(pp_ops)},
-        "decode_ms_per_token": round(tg_t / (args.gen * args.steps) * 1e3, 4),
+        "decode_ms_per_token": round(tok_s * 1e3, 4),
         "decode_bytes_per_token": int(tok_bytes),
-        "decode_effective_gbs": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9, 1),
-        "decode_frac_hbm_roofline": round(tok_bytes / (tg_t / (args.gen * args.steps)) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": roofline,
-        "eager_decode_kernel_ms": {k: round(v[0] / 5, 4) for k, v in prof.items()},
-        "eager_decode_step_ms": round(step_ms, 3),
+        "decode_effective_gbs": round(tok_bytes / tok_s / 1e9, 1),
+        "decode_frac_hbm_roofline": round(tok_bytes / tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "setup_s": {"synthesize": round(t_gen, 1), "upload": round(t_load, 1)},
         "greedy_head": [int(t) for t in toks[:8]],
     }
-    if not args.no_cpu_baseline and headline:
-        out["cpu_baseline"] = cpu_baseline(img, V, args)
-    print(json.dumps(out), flush=True)
+    extra = {}
+    if full:
+        # the same prefill fed in micro-batches of 1 and 128 tokens
+        def prefill_batched(bsz):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for p0 in range(0, n_prompt, bsz):
+                be.forward_argmax(prompt[p0:p0 + bsz], p0)
+            torch.cuda.synchronize()
+            return n_prompt / (time.perf_counter() - t)
+        by_batch = {str(bsz): round(prefill_batched(bsz), 1) for bsz in (1, 128)}
+        by_batch[str(n_prompt)] = round(pp_tps, 1)
+        extra["prefill_tok_s_by_batch"] = by_batch
+        # roofline of the dominant decode kernel, timed live with HIP events: the
+        # single-token gate/up/SwiGLU launch over every layer's weights in turn, on
+        # the backend's stream, so each launch streams its weights from HBM
+        roofline = None
+        if not spec.n_expert:
+            glu_us, glu_bytes = be.time_ffn_glu(reps=3)
+            achieved = glu_bytes / (glu_us / 1e6) / 1e9
+            dflt = name == DEFAULT_WORKLOAD
+            roofline = {"bound": "hbm", "kernel": "gemv_dec_kernel gate+up+SwiGLU (RMSNorm+quantization of x in the prologue, "
+                                                  "quantized hidden out)",
+                        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic() if dflt else None,
+                        "traffic_source": ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel, scaled by a 256 MiB copy: "
+                                           "profiles/gemv_dec_gate_up_glu_llama8b_q4_0_pmc.md (not measured in this run)")
+                        if dflt else None,
+                        "bytes_per_launch": glu_bytes, "avg_launch_us": round(glu_us, 2)}
+        extra["roofline"] = roofline
+        prof = be.profile_decode(ctx_mid, reps=5)
+        extra["eager_decode_kernel_ms"] = {k: round(v[0] / 5, 4) for k, v in prof.items()}
+        extra["eager_decode_step_ms"] = round(sum(v[0] for v in prof.values()) / 5, 3)
+    be.close()
+    return res, extra, img
+
+
+def long_context():
+    """The 32K-context workload: the 8B Q4_0 model, a 32768-token prompt fed in
+    512-token batches (Engine::eval_tokens chunking), then 128 greedy steps, with
+    Turbo4 and with f16 KV caches."""
+    import torch
+
+    import rust_interference_engine_amd as R
+    from rust_interference_engine_amd import gguf, synth
+
+    n_prompt, n_gen, mb = 32768, 128, 512
+    spec = synth.baseline_llama31_8b_q4_0(seed=1, ctx=n_prompt + n_gen + 128)
+    img = synth.build_array(spec)
+    costs = gguf.per_token_costs(img, 0)
+    V, L, kvd = spec.n_vocab, spec.n_layer, spec.n_head_kv * spec.head_dim
+    prompt = [(i * 7919 + 13) % V for i in range(n_prompt)]
+    # K and V bytes per cached position and layer: f16 rows, or Turbo4 rows of
+    # 64 code bytes plus a 2-byte scale per 128 values (turbo.rs:136-138)
+    kv_pos = {"turbo4": 2 * (kvd // 128) * 66, "f16": 2 * kvd * 2}
+    res = {"workload": "llama-3.1-8b-shaped q4_0, pp32768 in 512-token batches then greedy tg128",
+           "data": "synthetic: N(0,0.02) weights quantized to Q4_0, prompt ids (i*7919+13) mod V"}
+    for kvname, kv in (("turbo4", R.KvType.TURBO4), ("f16", R.KvType.F16)):
+        be = R.HipBackend(img, n_ctx=n_prompt + n_gen + 64, max_batch=mb, kv_type=kv)
+        be.forward_argmax(prompt[:8], 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for p0 in range(0, n_prompt, mb):
+            be.forward_argmax(prompt[p0:p0 + mb], p0)
+            if p0 % (16 * mb) == 0:
+                log(f"{kvname}: prefilled {p0 + mb} tokens")
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        toks = be.generate_greedy(n_prompt, n_gen)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        tok_s = (t2 - t1) / n_gen
+        tok_bytes = decode_bytes(costs, L, kv_pos[kvname], n_prompt + n_gen // 2 + 1)
+        res[kvname] = {"pp32768_tok_s": round(n_prompt / (t1 - t0), 1), "tg128_tok_s": round(n_gen / (t2 - t1), 2),
+                       "decode_bytes_per_token": int(tok_bytes),
+                       "decode_frac_hbm_roofline": round(tok_bytes / tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                       "kv_bytes": be.kv_bytes(), "greedy_head": [int(t) for t in toks[:8]]}
+        log(f"{kvname}: {res[kvname]}")
+        be.close()
+    return res
+
+
+def short_run(args):
+    """Counter and trace runs: prompts only, or decode steps only, on the headline image."""
+    import torch
+
+    import rust_interference_engine_amd as R
+    from rust_interference_engine_amd import synth
+
+    spec = getattr(synth, WORKLOADS[args.workload][0])(seed=1, ctx=8192)
+    img = synth.build_array(spec)
+    V = spec.n_vocab
+    be = R.HipBackend(img, n_ctx=args.prompt + args.gen + 64, max_batch=args.prompt, kv_type=R.KvType.F16)
+    prompt = [(i * 7919 + 13) % V for i in range(args.prompt)]
+    be.forward_argmax(prompt[:8], 0)
+    for _ in range(max(args.steps, 1)):
+        be.forward_argmax(prompt, 0)
+        if args.decode_only:
+            be.generate_greedy(args.prompt, args.gen)
+    torch.cuda.synchronize()
+    print(json.dumps({"short_run": args.workload, "prefill_only": args.prefill_only, "decode_only": args.decode_only,
+                      "steps": args.steps}), flush=True)
 
 
 def measured_traffic():
@@ -202,44 +321,6 @@ def measured_traffic():
     except OSError:
         pass
     return None
-
-
-def long_context(args):
-    """The 32K-context workload: the 8B Q4_0 model, a 32768-token prompt fed in
-    512-token batches (Engine::eval_tokens chunking), then 128 greedy steps, with
-    Turbo4 and with f16 KV caches.  One JSON line; not the bench line."""
-    import torch
-
-    import rust_interference_engine_amd as R
-    from rust_interference_engine_amd import synth
-
-    assert torch.cuda.is_available(), "needs the MI355X"
-    n_prompt, n_gen, mb = 32768, 128, 512
-    spec = synth.baseline_llama31_8b_q4_0(seed=1, ctx=n_prompt + n_gen + 128)
-    img = synth.build_array(spec)
-    V = spec.n_vocab
-    prompt = [(i * 7919 + 13) % V for i in range(n_prompt)]
-    res = {}
-    for name, kv in (("turbo4", R.KvType.TURBO4), ("f16", R.KvType.F16)):
-        be = R.HipBackend(img, n_ctx=n_prompt + n_gen + 64, max_batch=mb, kv_type=kv)
-        be.forward_argmax(prompt[:8], 0)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for p0 in range(0, n_prompt, mb):
-            be.forward_argmax(prompt[p0:p0 + mb], p0)
-            if p0 % (8 * mb) == 0:
-                print(f"{name}: prefilled {p0 + mb} tokens", file=sys.stderr, flush=True)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        toks = be.generate_greedy(n_prompt, n_gen)
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        res[name] = {"pp32768_tok_s": round(n_prompt / (t1 - t0), 1), "tg128_tok_s": round(n_gen / (t2 - t1), 2),
-                     "kv_bytes": be.kv_bytes(), "greedy_head": [int(t) for t in toks[:8]]}
-        print(f"{name}: {res[name]}", file=sys.stderr, flush=True)
-        be.close()
-    print(json.dumps({"metric": "pp32768 and tg128 tok/s at 32K context (Llama-3.1-8B Q4_0; Turbo4 vs f16 KV)", "n_gpus": 1,
-                      "data": "synthetic: N(0,0.02) weights quantized to Q4_0, prompt ids (i*7919+13) mod V", **res}), flush=True)
 
 
 def kernel_only(args):
@@ -264,14 +345,32 @@ def kernel_only(args):
     print(json.dumps({"ffn_glu_avg_us": round(us, 2), "bytes_per_launch": nb, "copy_bytes": n}), flush=True)
 
 
-def _cpu_model_name():
+def _cpu_model():
+    """The host CPU as lscpu names it (model name, family/model/stepping), and
+    whether it has the AVX2/FMA/F16C the reference's x86 kernels select."""
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k in ("Model name", "Vendor ID", "CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket",
+                     "Thread(s) per core", "CPU(s)"):
+                info[k] = v
+            if k == "Flags":
+                fl = set(v.split())
+                info["avx2_fma_f16c"] = {"avx2", "fma", "f16c"} <= fl
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    if "Model name" not in info:
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    info["Model name"] = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return info
 
 
 def _physical_cores():
@@ -290,43 +389,56 @@ def _physical_cores():
     return max(1, len(seen)), len(allowed)
 
 
-def cpu_baseline(img, V, args):
+def cpu_baseline(img, V):
     """RIE's CPU path (the oracle: a C restatement of RIE's x86 backend, AVX2
-    semantics, RIE's row chunking and fork/join pool) on the same GGUF image, at
+    semantics, RIE's row chunking and fork/join pool) on the headline image, at
     RIE's default of 8 threads (crates/rie-core/src/cpu.rs:100-102) and at every
-    physical core.  Bounded sample: Engine::bench's warm-up on 8 tokens, one
-    32-token prompt batch (whole 4-token tiles, as the 64-token chunks of RIE's
-    default -b 64: pp512 is extrapolated from its rate), then 6 greedy decode
-    steps at context 32-38 (the GPU's decode runs at 512-640; the KV share of the
-    bytes per token is under 2% at either length)."""
+    physical core.
+
+    Bounded sample of Engine::bench (engine.rs:540-564): the warm-up on 8 tokens,
+    the first 16 prompt tokens at positions 0-15 and the last 16 at positions
+    496-511, then 4 greedy decode steps at context 512-515.  The KV rows of
+    positions 16-495 stay zero, which changes no timing: a token's work depends
+    on its position, not on the cached values.  The prompt's matmuls run in
+    4-token tiles (kernels/matmul.rs:212-231), so a token's work is the same in a
+    16-, 64- (RIE's default -b 64) or 512-token batch (-b 512); only attention
+    grows, linearly with the position.  pp512 is therefore 512 over 512 times
+    the mean per-token time of the two chunks (the exact sum for a linear
+    per-token time), for -b 64 and -b 512 alike."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as O
 
     phys, allowed = _physical_cores()
     m = O.Model(img)
-    n_pp, n_gen = 32, 6
-    prompt = [(i * 7919 + 13) % V for i in range(n_pp)]
+    prompt = [(i * 7919 + 13) % V for i in range(512)]
+    n_chunk, n_gen = 16, 4
     runs = {}
     for threads in sorted({min(8, allowed), phys}):
-        b = O.Backend(m, 128, 64, O.KV_F16, n_threads=threads)
+        b = O.Backend(m, 640, 64, O.KV_F16, n_threads=threads)
         b.forward(prompt[:8], 0)  # warm-up (engine.rs:544-546)
         t0 = time.perf_counter()
-        logits = b.forward(prompt, 0)
+        b.forward(prompt[:n_chunk], 0)
         t1 = time.perf_counter()
+        logits = b.forward(prompt[512 - n_chunk:], 512 - n_chunk)
+        t2 = time.perf_counter()
         tok = O.argmax(logits)
         for i in range(n_gen):
-            logits = b.forward([tok], n_pp + i)
+            logits = b.forward([tok], 512 + i)
             tok = O.argmax(logits)
-        t2 = time.perf_counter()
-        runs[threads] = {"threads": threads, "pp32_tok_s": round(n_pp / (t1 - t0), 2),
-                         "pp512_tok_s_extrapolated": round(n_pp / (t1 - t0), 2), "tg_tok_s": round(n_gen / (t2 - t1), 3)}
+        t3 = time.perf_counter()
+        per_tok = ((t1 - t0) + (t2 - t1)) / (2 * n_chunk)
+        runs[threads] = {"threads": threads, "pp_tok_s_pos0": round(n_chunk / (t1 - t0), 3),
+                         "pp_tok_s_pos496": round(n_chunk / (t2 - t1), 3), "pp512_tok_s": round(1.0 / per_tok, 3),
+                         "tg_tok_s_ctx512": round(n_gen / (t3 - t2), 3)}
+        log(f"cpu baseline: {runs[threads]}")
         del b
     base = runs[min(8, allowed)]
-    return {"value": base["tg_tok_s"], "unit": "tok/s", "cores": base["threads"], "kind": "port",
-            "label": "RIE CPU path (C++ restatement)", "cpu_model": _cpu_model_name(), "nproc": os.cpu_count(),
+    return {"value": base["tg_tok_s_ctx512"], "unit": "tok/s", "cores": base["threads"], "kind": "port",
+            "label": "RIE CPU path (C++ restatement)", "cpu": _cpu_model(), "nproc": os.cpu_count(),
             "physical_cores_allowed": phys, "runs": list(runs.values()),
-            "sample": "same image; warm-up on 8 tokens, one 32-token prompt batch (pp512 extrapolated from its rate), "
-                      "then 6 greedy decode steps at context 32-38; value = decode tok/s at 8 threads"}
+            "sample": "headline image; warm-up on 8 tokens, prompt tokens 0-15 and 496-511 (pp512 for -b 64 and -b 512 "
+                      "from their mean per-token time), then 4 greedy decode steps at context 512-515; "
+                      "value = decode tok/s at 8 threads"}
 
 
 if __name__ == "__main__":
