@@ -137,7 +137,9 @@ int32_t rie_hip_quantize(int32_t ty, const float *x, size_t n, uint8_t *out);
 /* ---- parity hooks (no counterpart in the reference; for tests and debugging) ---- */
 /* Keep per-layer copies of intermediate f32 tensors during forward (slow path):
  * what = 0 x after attention, 1 x after FFN, 2 attention output, 3 q after
- * RoPE/scale, 4 k after norm/RoPE, 5 v, 6 FFN gated hidden, 7 MoE router logits. */
+ * RoPE/scale, 4 k after norm/RoPE, 5 v, 6 FFN gated hidden, 7 MoE router logits,
+ * 8 the experts the device routing selected ([n][k] int32 bit patterns, ascending),
+ * 9 their combination weights ([n][k]). */
 int32_t rie_hip_set_capture(rie_hip_backend *b, int32_t on);
 /* on = 1: single-token attention always splits the context into ranges merged
  * across workgroups, also at the short contexts where it otherwise runs one

@@ -249,7 +249,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         d_moe_tile_r0_ = dalloc<int>(allocs_, moe_max_tiles_);
         d_moe_ntiles_ = dalloc<int>(allocs_, 1);
     }
-    cap_.resize(8);
+    cap_.resize(10);
     RIE_HIP_CHECK(hipDeviceSynchronize());
 }
 
@@ -659,6 +659,15 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
     }
     if (!routed) launch_moe_route(d_router_, n, ne, k, L.norm_topk, L.unit_weights, d_moe_sel_, d_moe_w_, st_);
     check_launch("moe route");
+    if (capture_ && !in_capture_) {  // the routing the device applied: selected experts (int bits) and weights
+        RIE_HIP_CHECK(hipStreamSynchronize(st_));
+        for (int w = 8; w < 10; w++) {
+            cap_[w].resize(c.n_layer);
+            cap_[w][cur_layer_].resize((size_t)n * k);
+        }
+        RIE_HIP_CHECK(hipMemcpy(cap_[8][cur_layer_].data(), d_moe_sel_, (size_t)n * k * 4, hipMemcpyDeviceToHost));
+        RIE_HIP_CHECK(hipMemcpy(cap_[9][cur_layer_].data(), d_moe_w_, (size_t)n * k * 4, hipMemcpyDeviceToHost));
+    }
     mark("moe_route");
     if (!self_norm) RIE_HIP_CHECK(hipMemcpyAsync(d_moe_xn_, d_xn_, (size_t)n * E * 4, hipMemcpyDeviceToDevice, st_));
     if (n == 1) {

@@ -71,9 +71,22 @@ class NaiveModel:
             xq = G.dequant_act(ty, x) if self.emulate else x
             return (w.astype(np.float64) @ xq.astype(np.float64)).astype(np.float32)
 
+        # per-dimension frequency factors (Llama-3.1 rope_freqs.weight, else Phi-3's
+        # rope_factors_short.weight): inv_freq[i] /= factor[i] where the factor is
+        # nonzero (Rope::new, ops.rs:65-78; Model::load, model/mod.rs:130-133)
+        fac_t = self.t("rope_freqs.weight")
+        if fac_t is None:
+            fac_t = self.t("rope_factors_short.weight")
+        factors = None if fac_t is None else fac_t[0].reshape(-1).astype(np.float32)
+
         def rope(x, pos, base):
             i = np.arange(rd // 2)
             inv = np.power(np.float32(base), (np.float32(-2.0) * i.astype(np.float32) / np.float32(rd)), dtype=np.float32)
+            if factors is not None:
+                f = np.ones(rd // 2, np.float32)
+                m = min(len(f), len(factors))
+                f[:m] = np.where(factors[:m] != 0, factors[:m], np.float32(1))
+                inv = (inv / f).astype(np.float32)
             th = (np.float32(pos) * inv).astype(np.float32)
             s, c = np.sin(th).astype(np.float32), np.cos(th).astype(np.float32)
             if neox:

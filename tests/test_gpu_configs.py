@@ -23,13 +23,22 @@ orders, and every later activation quantizer turns those last-bit differences
 into whole-step code flips near its rounding boundaries, so the logits of a
 random-weight model with a 128K-152K vocabulary drift apart by about 1% within
 two layers, and routed-expert choices flip where two router logits nearly tie.
-Greedy agreement is therefore asserted outside near-ties: a teacher-forced
-step may pick another token only where the CPU's top-2 logit margin is within
-twice that step's largest logit difference, and the free-running sequences must
-be identical up to the first step whose CPU top-2 margin is within twice the
-largest logit difference seen.  The measured figures (and the count of
-identical free-running steps) are appended to gpurun_out/parity_records.jsonl
-when that directory can be written.
+
+The yardstick for that drift is the reference path's own sensitivity: a
+control runs the CPU path on the image with one layer-0 RMSNorm weight moved by
+one ulp (1.0 -> 1.0000001), in lockstep with the other two.  The GPU's distance
+from the CPU must stay within twice the control's (prompt logits; the medians of
+the teacher-forced steps; their maxima for the dense shapes).  Greedy agreement
+is asserted outside near-ties: a teacher-forced step may pick another token
+only where the CPU's top-2 logit margin is within twice the step's largest
+logit difference (GPU's or control's), and the free-running sequences must be
+identical up to the first step whose CPU top-2 margin lies within twice the
+largest logit difference seen on the GPU or the control side.  With experts,
+the routing the GPU applied (selected experts and weights, read back) must equal
+the oracle's routing of the GPU's own router logits, and rows or steps are
+excused only on that checked routing.  The measured figures (counts of
+identical free-running steps for the GPU and the control included) are appended
+to gpurun_out/parity_records.jsonl when that directory can be written.
 """
 import json
 import os
@@ -94,45 +103,48 @@ def _top2(x):
     return float(a[1] - a[0])
 
 
-def _routing_flips(gr, orr, k):
-    """Per token: does the GPU's top-k expert set (router logits gr, ties to the
-    lower index, cpu.rs:495) differ from the CPU's, and if so is it at a near-tie
-    (the CPU's k-th minus (k+1)-th logit within twice the largest router logit
-    difference)?  Returns (differs, excused) boolean arrays."""
-    n = orr.shape[0]
-    differs, excused = np.zeros(n, bool), np.zeros(n, bool)
-    for t in range(n):
-        ids = np.arange(orr.shape[1])
-        sg = set(np.lexsort((ids, -gr[t]))[:k].tolist())
-        so = np.lexsort((ids, -orr[t]))
-        if sg != set(so[:k].tolist()):
-            differs[t] = True
-            margin = float(orr[t, so[k - 1]] - orr[t, so[k]])
-            excused[t] = margin <= 2 * float(np.abs(gr[t] - orr[t]).max())
-    return differs, excused
+# Qwen3-MoE routing flags: top-k weights renormalized, not unit (config.rs:167)
+MOE_NORM_TOPK, MOE_UNIT_WEIGHTS = True, False
 
 
-def _routing_explains(g, o, L, n, ne, k, rows, row_err):
+def _applied_routing(oracle, g, il, gr, n, k):
+    """The experts and weights the device routing applied in layer il (capture
+    slots 8 and 9), checked against the oracle's routing (model/cpu.rs:492-500)
+    of the GPU's own router logits gr: the selection bit-exact, the weights to f32
+    rounding (the device's expf against glibc's)."""
+    gsel = g.capture(il, 8, n * k).view(np.int32).reshape(n, k)
+    gw = g.capture(il, 9, n * k).reshape(n, k)
+    want_s, want_w = oracle.moe_route(gr, k, MOE_NORM_TOPK, MOE_UNIT_WEIGHTS)
+    assert np.array_equal(gsel, want_s), f"layer {il}: device routing selected {np.argwhere(gsel != want_s)[:4]} differently"
+    np.testing.assert_allclose(gw, want_w, rtol=4e-6, atol=1e-8, err_msg=f"layer {il}: device routing weights")
+    return gsel, gw
+
+
+def _routing_explains(oracle, g, o, L, n, ne, k, rows, row_err):
     """rows (token indices of the last forward) whose result is off by row_err
-    (relative): True when each of them, in some layer, took a different expert
-    set than the CPU at a router near-tie, or kept the set but had its
-    combination weights (softmax over the top k, renormalized, cpu.rs:496-501)
-    moved by at least a quarter of its error.  Router logits of N(0, 1) gate
-    weights have a standard deviation of √E (45 at E 2048), so the last-bit
-    drift of x moves them by tenths and the weights by tens of percent."""
+    (relative): True when each of them, in some layer, was combined from another
+    expert set than the CPU's at a router near-tie (the CPU's k-th minus (k+1)-th
+    logit within twice the largest router logit difference), or from the same set
+    with weights moved by at least a quarter of its error.  The GPU side is the
+    routing it applied, read back and checked against the oracle's routing of its
+    router logits; the CPU side is the oracle's routing of its own.  Router logits
+    of N(0, 1) gate weights have a standard deviation of √E (45 at E 2048), so the
+    last-bit drift of x moves them by tenths and the weights by tens of percent."""
     explained = np.zeros(n, bool)
     for il in range(L):
         gr, orr = g.capture(il, 7, n * ne).reshape(n, ne), o.capture(il, 7).reshape(n, ne)
-        d, ex = _routing_flips(gr, orr, k)
-        assert np.all(ex[d]), f"layer {il}: expert choice differs without a router near-tie at tokens {np.where(d & ~ex)[0]}"
-        explained |= d
+        gsel, gw = _applied_routing(oracle, g, il, gr, n, k)
+        osel, ow = oracle.moe_route(orr, k, MOE_NORM_TOPK, MOE_UNIT_WEIGHTS)
+        noise = np.abs(gr - orr).max(axis=1)
+        for t in range(n):
+            if not np.array_equal(gsel[t], osel[t]):
+                so = np.lexsort((np.arange(ne), -orr[t]))
+                margin = float(orr[t, so[k - 1]] - orr[t, so[k]])
+                assert margin <= 2 * float(noise[t]), \
+                    f"layer {il} token {t}: expert choice differs without a router near-tie (margin {margin})"
+                explained[t] = True
         for t, err in zip(rows, row_err):
-            if d[t]:
-                continue
-            sel = np.lexsort((np.arange(ne), -orr[t]))[:k]
-            wg = np.exp(gr[t, sel].astype(np.float64) - gr[t, sel].max())
-            wo = np.exp(orr[t, sel].astype(np.float64) - orr[t, sel].max())
-            if np.abs(wg / wg.sum() - wo / wo.sum()).max() >= err / 4:
+            if not explained[t] and np.array_equal(gsel[t], osel[t]) and np.abs(gw[t] - ow[t]).max() >= err / 4:
                 explained[t] = True
     return bool(np.all(explained[rows]))
 
@@ -144,8 +156,11 @@ def test_workload_shape_matches_oracle(oracle, name):
     img = synth.build(spec)
     nv, E, L = spec.n_vocab, spec.n_embd, spec.n_layer
     n_ctx = N_PROMPT + N_FREE + 64
+    threads = min(16, os.cpu_count() or 1)
     g = R.HipBackend(img, n_ctx=n_ctx, max_batch=N_PROMPT)
-    o = oracle.Backend(oracle.Model(img), n_ctx, N_PROMPT, 0, n_threads=min(16, os.cpu_count() or 1))
+    o = oracle.Backend(oracle.Model(img), n_ctx, N_PROMPT, 0, n_threads=threads)
+    # the control: the reference path on the image with one layer-0 norm weight moved by one ulp
+    c = oracle.Backend(oracle.Model(_one_ulp_image(img)), n_ctx, N_PROMPT, 0, n_threads=threads)
     prompt = _prompt(7, N_PROMPT, nv)
     print(f"{name}: prompt of {N_PROMPT} as one batch", flush=True)
 
@@ -154,81 +169,124 @@ def test_workload_shape_matches_oracle(oracle, name):
     o.set_capture(True)
     lg = g.forward(prompt, 0)
     lo = o.forward(prompt, 0)
+    lc = c.forward(prompt, 0)
     xg = g.capture(L - 1, 1, N_PROMPT * E).reshape(N_PROMPT, E)
     xo = o.capture(L - 1, 1).reshape(N_PROMPT, E)
+    if spec.n_expert:  # the routing the device applied to every prompt token in every layer, checked
+        for il in range(L):
+            gr = g.capture(il, 7, N_PROMPT * spec.n_expert).reshape(N_PROMPT, spec.n_expert)
+            _applied_routing(oracle, g, il, gr, N_PROMPT, spec.n_expert_used)
     row_rel = np.abs(xg - xo).max(axis=1) / np.abs(xo).max(axis=1)
     off = np.where(row_rel >= 0.05)[0]
     explained = bool(spec.n_expert and off.size and
-                     _routing_explains(g, o, L, N_PROMPT, spec.n_expert, spec.n_expert_used, off, row_rel[off]))
+                     _routing_explains(oracle, g, o, L, N_PROMPT, spec.n_expert, spec.n_expert_used, off, row_rel[off]))
     g.set_capture(False)
     o.set_capture(False)
-    m0 = logit_metrics(lg, lo)
+    m0, mc0 = logit_metrics(lg, lo), logit_metrics(lc, lo)
     rec = {"config": name, "layers": L, "hidden": E, "vocab": nv, "prompt_rows_max_rel": float(row_rel.max()),
            "prompt_rows_median_rel": float(np.median(row_rel)), "prompt_rows_over_0.03": int((row_rel >= 0.03).sum()),
-           "prompt_logits": m0}
+           "prompt_logits": m0, "control_prompt_logits": mc0}
     print(f"{name}: {rec}", flush=True)
     # residual rows after the last layer: the same drift as the logits, per token; with
     # experts, a token whose top-k flipped on a router near-tie (checked) takes other experts
     assert np.median(row_rel) < 0.02, rec
     assert off.size == 0 or explained, f"{name}: prompt rows {off} off by up to {row_rel.max()} without an expert-choice flip"
     assert m0["max_rel"] < 0.03 and m0["kl"] < 1e-3, (name, m0)
+    assert m0["max_rel"] <= 2 * mc0["max_rel"] and m0["kl"] <= 2 * mc0["kl"], (name, m0, mc0)
 
     # ---- teacher-forced decode through the replayed graph: the CPU's token each step
-    tf, agree, bad = [], 0, []
+    tf, ctl, agree, agree_c, bad = [], [], 0, 0, []
     for step in range(N_TF):
         tok = oracle.argmax(lo)
+        agree_c += int(oracle.argmax(lc) == tok)
         if R.argmax(lg) == tok:
             agree += 1
         else:
-            bad.append((step, _top2(lo), float(np.abs(lg - lo).max())))
+            bad.append((step, _top2(lo), float(np.abs(lg - lo).max()), float(np.abs(lc - lo).max())))
         pos = N_PROMPT + step
-        lg, lo = g.forward([tok], pos), o.forward([tok], pos)
+        lg, lo, lc = g.forward([tok], pos), o.forward([tok], pos), c.forward([tok], pos)
         m = logit_metrics(lg, lo)
+        ctl.append(logit_metrics(lc, lo))
         m["routing_flip"] = False
         if spec.n_expert and (m["max_rel"] >= 0.03 or m["kl"] >= 1e-3):
-            # the same step again with the router logits captured (the same cache rows are
-            # rewritten with the same bits; capture mode's logits equal the graph's bitwise)
+            # the same step again with the router logits and the applied routing captured
+            # (the same cache rows are rewritten with the same bits; capture mode's logits
+            # equal the graph's bitwise)
             g.set_capture(True)
             o.set_capture(True)
             lg2, lo2 = g.forward([tok], pos), o.forward([tok], pos)
             assert np.array_equal(lo2, lo) and np.array_equal(lg2, lg), "step not reproducible"
-            m["routing_flip"] = _routing_explains(g, o, L, 1, spec.n_expert, spec.n_expert_used, [0],
+            m["routing_flip"] = _routing_explains(oracle, g, o, L, 1, spec.n_expert, spec.n_expert_used, [0],
                                                   [max(m["max_rel"], 0.03)])
             g.set_capture(False)
             o.set_capture(False)
         tf.append(m)
-    plain = [m for m in tf if not m["routing_flip"]]  # steps whose expert weights moved are excused
+    plain = [m for m in tf if not m["routing_flip"]]  # steps whose checked expert weights moved are excused
     rec["decode_max_rel"] = max(m["max_rel"] for m in plain)
     rec["decode_max_abs"] = max(m["max_abs"] for m in plain)
     rec["decode_max_kl"] = max(m["kl"] for m in plain)
     rec["decode_median_kl"] = float(np.median([m["kl"] for m in tf]))
+    rec["decode_median_max_rel"] = float(np.median([m["max_rel"] for m in tf]))
     rec["decode_steps_with_expert_flip"] = [i for i, m in enumerate(tf) if m["routing_flip"]]
     rec["teacher_forced_argmax_agree"] = f"{agree}/{N_TF}"
-    rec["teacher_forced_disagreements"] = [(i, round(mg, 5), round(d, 5)) for i, mg, d in bad]
+    rec["teacher_forced_disagreements"] = [(i, round(mg, 5), round(d, 5)) for i, mg, d, _ in bad]
+    rec["control_decode_max_rel"] = max(m["max_rel"] for m in ctl)
+    rec["control_decode_max_kl"] = max(m["kl"] for m in ctl)
+    rec["control_decode_median_kl"] = float(np.median([m["kl"] for m in ctl]))
+    rec["control_decode_median_max_rel"] = float(np.median([m["max_rel"] for m in ctl]))
+    rec["control_teacher_forced_argmax_agree"] = f"{agree_c}/{N_TF}"
     print(f"{name}: {rec}", flush=True)
     assert rec["decode_max_rel"] < 0.03 and rec["decode_max_kl"] < 1e-3, rec
-    for i, mg, d in bad:  # a different choice only inside the noise band (or after an expert flip)
-        assert mg <= 2 * d or (i > 0 and tf[i - 1]["routing_flip"]), \
-            f"{name}: teacher-forced step {i}: cpu margin {mg} exceeds 2x logit difference {d}"
+    # within the reference path's own last-bit sensitivity: medians everywhere; maxima
+    # of the dense shapes (a routed shape's maximum is the step with an expert flip,
+    # on either side)
+    assert rec["decode_median_kl"] <= 2 * rec["control_decode_median_kl"], rec
+    assert rec["decode_median_max_rel"] <= 2 * rec["control_decode_median_max_rel"], rec
+    if not spec.n_expert:
+        assert rec["decode_max_kl"] <= 2 * rec["control_decode_max_kl"], rec
+        assert rec["decode_max_rel"] <= 2 * rec["control_decode_max_rel"], rec
+    for i, mg, d, dc in bad:  # a different choice only inside the noise band (or after an expert flip)
+        assert mg <= 2 * max(d, dc) or (i > 0 and tf[i - 1]["routing_flip"]), \
+            f"{name}: teacher-forced step {i}: cpu margin {mg} exceeds 2x logit difference {max(d, dc)}"
 
-    # ---- 128 free-running greedy steps on both sides
+    # ---- 128 free-running greedy steps on the GPU, the CPU path and the control
     want, margins, _ = o.greedy(prompt, N_FREE, N_PROMPT)
+    want_c, _, _ = c.greedy(prompt, N_FREE, N_PROMPT)
     first = g.forward_argmax(prompt, 0)
     got = g.generate_greedy(N_PROMPT, N_FREE)
     assert int(got[0]) == first
     noise = max([m0["max_abs"]] + [m["max_abs"] for m in tf])
+    noise_c = max([mc0["max_abs"]] + [m["max_abs"] for m in ctl])
     diverge = next((i for i in range(N_FREE) if int(got[i]) != int(want[i])), None)
+    diverge_c = next((i for i in range(N_FREE) if int(want_c[i]) != int(want[i])), None)
     near_tie = next((i for i in range(N_FREE) if margins[i] <= 2 * noise), None)
+    near_tie_c = next((i for i in range(N_FREE) if margins[i] <= 2 * noise_c), None)
     rec["greedy_steps_identical"] = N_FREE if diverge is None else diverge
     rec["greedy_first_near_tie"] = near_tie
+    rec["control_greedy_steps_identical"] = N_FREE if diverge_c is None else diverge_c
+    rec["control_greedy_first_near_tie"] = near_tie_c
     if diverge is not None:
         rec["divergence_top2_margin"] = float(margins[diverge])
     _record(rec)
     print(f"{name}: {rec}", flush=True)
+    # the GPU's sequence leaves the CPU's no earlier than the control's noise band first
+    # admits a flip: the step where the reference path itself, moved by one ulp, could
     if diverge is not None:
-        assert near_tie is not None and diverge >= near_tie, \
-            f"{name}: greedy sequences differ from step {diverge} (cpu top-2 margin {margins[diverge]}, noise {noise})"
+        band = [x for x in (near_tie, near_tie_c) if x is not None]
+        assert band and diverge >= min(band), \
+            f"{name}: greedy sequences differ from step {diverge} (cpu top-2 margin {margins[diverge]}, noise {noise}, control noise {noise_c})"
     g.close()
+
+
+def _one_ulp_image(img):
+    """The image with blk.0.attn_norm.weight[0] moved from 1.0 to the next float up."""
+    from rust_interference_engine_amd import gguf
+    img2 = bytearray(img)
+    off = gguf.tensor_offset(img, "blk.0.attn_norm.weight")
+    w = np.frombuffer(img2, np.float32, count=1, offset=off)
+    assert w[0] == 1.0
+    w[:] = np.nextafter(np.float32(1.0), np.float32(2.0))
+    return bytes(img2)
 
 
 LEVELS_I8 = np.array([-126, -95, -74, -58, -43, -30, -18, -6, 6, 18, 30, 43, 58, 74, 95, 126], np.float64)  # turbo.rs:126
@@ -348,17 +406,13 @@ def test_full_depth_llama8b_within_reference_sensitivity(oracle):
     assert torch.cuda.is_available(), "needs the MI355X"
     spec = synth.baseline_llama31_8b_q4_0()
     img = synth.build(spec)
-    img2 = bytearray(img)
-    off = gguf.tensor_offset(img, "blk.0.attn_norm.weight")
-    w0 = np.frombuffer(img2, np.float32, count=1, offset=off)
-    assert w0[0] == 1.0
-    np.frombuffer(img2, np.float32, count=1, offset=off)[:] = np.nextafter(np.float32(1.0), np.float32(2.0))
+    img2 = _one_ulp_image(img)
     nv = spec.n_vocab
     n_ctx = N_DEEP_PROMPT + N_DEEP_TF + 8
     threads = min(16, os.cpu_count() or 1)
     g = R.HipBackend(img, n_ctx=n_ctx, max_batch=N_DEEP_PROMPT)
     o = oracle.Backend(oracle.Model(img), n_ctx, N_DEEP_PROMPT, 0, n_threads=threads)
-    c = oracle.Backend(oracle.Model(bytes(img2)), n_ctx, N_DEEP_PROMPT, 0, n_threads=threads)
+    c = oracle.Backend(oracle.Model(img2), n_ctx, N_DEEP_PROMPT, 0, n_threads=threads)
     prompt = _prompt(7, N_DEEP_PROMPT, nv)
     print(f"llama8b, 32 layers: prompt of {N_DEEP_PROMPT} as one batch", flush=True)
     lg, lo, lc = g.forward(prompt, 0), o.forward(prompt, 0), c.forward(prompt, 0)

@@ -816,6 +816,31 @@ def test_hidden_and_error_contract(oracle, cuda):
         g.forward([1, 2], 0, logits=np.zeros(10, np.float32))
 
 
+@pytest.mark.parametrize("ty,tol", [(F16, 3e-3), (Q4_0, 0.03)])
+def test_rope_frequency_factors_match_oracle(oracle, cuda, ty, tol):
+    """A tiny llama carrying rope_freqs.weight (Llama-3.1's per-dimension RoPE
+    factors, Rope::new ops.rs:65-78): an 11-token prompt as one batch (prompt
+    head prep and attention), then 24 teacher-forced single-token steps (the
+    fused decode attention, graph replay), logits against the oracle at the
+    reference's whole-model tolerances (tests/model.rs:340-375)."""
+    from naive_model import max_rel_err
+    from test_oracle_model import rope_factor_image
+    spec, _, img = rope_factor_image(oracle, ty)
+    g = R.HipBackend(img, n_ctx=64, max_batch=16)
+    o = oracle.Backend(oracle.Model(img), 64, 16, 0, n_threads=4)
+    nv = spec.n_vocab
+    prompt = [(i * 37 + 5) % nv for i in range(11)]
+    lg, lo = g.forward(prompt, 0), o.forward(prompt, 0)
+    assert max_rel_err(lg, lo) < tol
+    for step in range(24):
+        tok = oracle.argmax(lo)
+        pos = len(prompt) + step
+        lg, lo = g.forward([tok], pos), o.forward([tok], pos)
+        err = max_rel_err(lg, lo)
+        assert err < tol, (step, err)
+    g.close()
+
+
 @pytest.mark.parametrize("ty", [Q4_0, Q4_K])
 def test_hidden_after_graph_replayed_decode_steps(cuda, ty):
     """Backend::hidden (model/mod.rs:314-319; read every decode step by the

@@ -170,3 +170,40 @@ def test_forward_error_contract(oracle):
             be.forward(toks, pos)
     with pytest.raises(oracle.OracleError, match="logits buffer too small"):
         be.forward([1, 2], 0, logits=np.zeros(10, np.float32))
+
+
+def rope_factor_image(oracle, wtype):
+    """A tiny llama image carrying rope_freqs.weight (Llama-3.1's per-dimension
+    RoPE factors): every other dimension pair slowed by 1.5-8x, one zero factor
+    (left out by Rope::new, ops.rs:69-73)."""
+    from gguf_edit import add_f32_tensor
+    spec = oracle.synth_spec("tiny-llama", wtype)
+    base = oracle.synth_build(spec)
+    half = spec.rope_dim // 2
+    fac = np.ones(half, np.float32)
+    fac[::2] = np.array([1.5, 2.0, 3.0, 4.0, 8.0], np.float32)[np.arange(len(fac[::2])) % 5]
+    fac[1] = 0.0
+    return spec, base, add_f32_tensor(base, "rope_freqs.weight", fac)
+
+
+def test_rope_frequency_factors(oracle):
+    """rope_freqs.weight (Model::load, model/mod.rs:130-133; Rope::new,
+    ops.rs:65-78): the oracle on an image carrying the factors agrees with the
+    naive model that applies them, within the F32 whole-model tolerance, and the
+    factors move the logits well past it (so the path is exercised)."""
+    spec, base, img = rope_factor_image(oracle, F32)
+    nv = spec.n_vocab
+    tokens = [(i * 37 + 5) % nv for i in range(13)]
+    expect = NaiveModel(img, emulate_act_quant=True).logits(tokens)
+    be = oracle.Backend(oracle.Model(img), 64, 4, n_threads=3)
+    plain = oracle.Backend(oracle.Model(base), 64, 4, n_threads=3)
+    moved = 0.0
+    for pos in range(0, len(tokens), 4):
+        chunk = tokens[pos:pos + 4]
+        lg = be.forward(chunk, pos, all_logits=True)
+        lp = plain.forward(chunk, pos, all_logits=True)
+        for t in range(len(chunk)):
+            err = max_rel_err(lg[t * nv:(t + 1) * nv], expect[pos + t])
+            assert err < 2e-3, f"token {pos + t}: rel err {err}"
+            moved = max(moved, max_rel_err(lp[t * nv:(t + 1) * nv], lg[t * nv:(t + 1) * nv]))
+    assert moved > 0.05, f"the factors moved the logits by only {moved}"
