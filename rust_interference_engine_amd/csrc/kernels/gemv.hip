@@ -288,7 +288,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     // the loads in program order waits with it: with every wave's weight loads
     // ahead of the prologue, the activation was ready 8 µs (median) into the
     // gate/up launch, against ~2 µs for the x loads alone.
-    constexpr bool SPLIT = PRO8 && NT == 512;
+    constexpr bool SPLIT = PRO8 && NT >= 512;
     __shared__ int s_arrive;  // SPLIT: arrivals of waves 0-3 (4: norm sums, 8: activation)
     if constexpr (SPLIT) {
         if (tid == 0) s_arrive = 0;
@@ -716,10 +716,14 @@ static bool plan_dec(DecP &p, int &lpr, int &upl, int &nt, size_t &lds, int &blo
     nt = 256;
     if (p.glu && p.hq.qs) {
         if (p.total_rows % 32) return false;
-        // whole Q8_0 blocks of h per workgroup, in one pass: 512 or 1024 threads
-        if (pass < 32) {
-            nt = 256 * (32 / pass);
-            pass = 32;
+        // whole Q8_0 blocks of h per workgroup, in one pass: 512 or 1024 threads.
+        // 64 rows (one workgroup per CU) where 32-row workgroups would number more
+        // than the 256 CUs: a CU's second workgroup would request its activation
+        // behind the first one's weight stream
+        const int want = (!p.xsel && p.total_rows % 64 == 0 && p.total_rows / 32 > 256) ? 64 : 32;
+        if (pass < want) {
+            nt = 256 * (want / pass);
+            pass = want;
         }
         m = 1;
         if (nt > 1024) return false;
