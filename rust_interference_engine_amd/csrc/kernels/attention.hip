@@ -1258,21 +1258,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
         }
     }
     __shared__ int s_last;
-    // Publication of the partials: every thread's stores complete before the
-    // barrier, and the arrival count is an agent-scope release, so in the HIP
-    // memory model the stores of all ranges happen-before the last arrival's
-    // acquire fence and the merge's loads after it (barrier, then release
-    // read-modify-write, then acquire fence on the value it returned).
+    // Publication of the partials.  They are agent-scope atomic stores (written
+    // through to the device coherence point), every thread waits for their
+    // completion before the barrier, and the merge reads them only with
+    // agent-scope atomic loads (read from that point), so the arrival count is a
+    // relaxed agent-scope add issued after the barrier, and the last arrival's
+    // loads issue after the add has returned.  An agent-scope release or acquire
+    // would add a write-back or an invalidation of the whole L2 of the XCD
+    // (buffer_wbl2 / buffer_inv), which only plain stores and loads need.
     wait_vmem();
     __syncthreads();
     if (tid == 0) {
         int *cnt = a.counters + blockIdx.y * ATT_CNT_STRIDE;  // one 128-byte line per head slice: no contention between slices
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == ns - 1;
-        if (old == ns - 1) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (old == ns - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
