@@ -289,6 +289,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     // ahead of the prologue, the activation was ready 8 µs (median) into the
     // gate/up launch, against ~2 µs for the x loads alone.
     constexpr bool SPLIT = PRO8 && NT >= 512;
+    constexpr bool ROUTER = TY == T_F32 && !GLU;  // may carry the MoE routing (p.route)
     __shared__ int s_arrive;  // SPLIT: arrivals of waves 0-3 (4: norm sums, 8: activation)
     if constexpr (SPLIT) {
         if (tid == 0) s_arrive = 0;
@@ -629,6 +630,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
             if constexpr (GLU) v = (p.glu == 2 ? gelu_tanh_f(sum) : silu_f(sum)) * sum2;
             float *out = p.seg[sg].out;
             if (p.seg[sg].epi == EPI_ADD) out[r] = (ep_pre && i == ep_i0 ? ep_res : out[r]) + v;
+            else if (ROUTER && p.route.cnt) st_coh(out + r, v);  // read by the routing workgroup
             else out[r] = v;
             hv[i] = v;
         }
@@ -659,23 +661,25 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     }
 }
 
-// The router GEMV's last workgroup routes the token: every workgroup counts its
-// stored logits with an agent-scope release; the last one to arrive takes an
-// agent-scope acquire, re-arms the counter and runs the routing in its first wave.
+// The router GEMV's last workgroup routes the token.  The logits are agent-scope
+// atomic stores (written through to the device coherence point); every thread
+// waits for their completion before the barrier, so the arrival count is a
+// relaxed agent-scope add, and the last workgroup to arrive re-arms the counter
+// and runs the routing in its first wave, reading the logits with agent-scope
+// atomic loads.  No release or acquire: those add a write-back or invalidation of
+// the whole L2 of the XCD, which only plain stores and loads need.
 __device__ __forceinline__ void route_last_workgroup(const DecP &p) {
     __shared__ int s_last;
+    wait_vmem();
     __syncthreads();  // the workgroup's logits are stored
     if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(p.route.cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(p.route.cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == (int)gridDim.x - 1;
-        if (s_last) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __hip_atomic_store(p.route.cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (s_last) __hip_atomic_store(p.route.cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (s_last && threadIdx.x < 64)
-        moe_route_wave(p.seg[0].out, p.route.n_exp, p.route.k, p.route.norm_topk, p.route.unit_weights, p.route.sel, p.route.wgt);
+        moe_route_wave<true>(p.seg[0].out, p.route.n_exp, p.route.k, p.route.norm_topk, p.route.unit_weights, p.route.sel, p.route.wgt);
 }
 
 template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8 = false, bool PROQ = false>

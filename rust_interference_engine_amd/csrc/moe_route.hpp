@@ -26,7 +26,9 @@ __device__ __forceinline__ float row_max16(float v) {
 }
 // One wavefront routes one token: l holds its n_exp logits; sel/wgt receive its k
 // choices in ascending expert order.  NE = experts per lane (n_exp ≤ 64·NE).
-template <int NE>
+// COH: the logits were published by other workgroups of the same launch with
+// agent-scope atomic stores, so they are read with agent-scope atomic loads.
+template <int NE, bool COH>
 __device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt) {
     const int lane = threadIdx.x & 63;
     float pr[NE];
@@ -34,7 +36,7 @@ __device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int 
 #pragma unroll
     for (int i = 0; i < NE; i++) {
         const int e = lane + 64 * i;
-        pr[i] = e < n_exp ? l[e] : -INFINITY;
+        pr[i] = e < n_exp ? (COH ? ld_coh(l + e) : l[e]) : -INFINITY;
         mx = fmaxf(mx, pr[i]);
     }
     mx = wave_max(mx, 64);
@@ -101,11 +103,12 @@ __device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int 
         wgt[rank] = unit_weights ? 1.0f : my_v / norm;
     }
 }
+template <bool COH = false>
 __device__ __forceinline__ void moe_route_wave(const float *l, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt) {
-    if (n_exp <= 64) moe_route_wave_t<1>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
-    else if (n_exp <= 128) moe_route_wave_t<2>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
-    else if (n_exp <= 256) moe_route_wave_t<4>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
-    else moe_route_wave_t<8>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    if (n_exp <= 64) moe_route_wave_t<1, COH>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else if (n_exp <= 128) moe_route_wave_t<2, COH>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else if (n_exp <= 256) moe_route_wave_t<4, COH>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
+    else moe_route_wave_t<8, COH>(l, n_exp, k, norm_topk, unit_weights, sel, wgt);
 }
 
 
