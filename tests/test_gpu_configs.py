@@ -326,6 +326,7 @@ def test_long_context_attention(oracle, kv):
     g = R.HipBackend(img, n_ctx=n_ctx, max_batch=mb, kv_type=kv)
     prompt = _prompt(11, n_prompt + 3, nv)
     sampled = {0, 31 * mb, n_prompt - mb}
+    worst_prompt = 0.0
     for p0 in range(0, n_prompt, mb):
         cap = p0 in sampled
         g.set_capture(cap)
@@ -344,44 +345,71 @@ def test_long_context_attention(oracle, kv):
                         ref = oracle.turbo_quantize(src[t, h])
                         assert np.array_equal(rows[h, p0 + t], ref[2:]), (p0 + t, h)
                         assert scales[h, p0 + t] == ref[:2].view(np.uint16)[0], (p0 + t, h)
+        # the batch's attention outputs (at 16K and 32K the prompt kernel runs over
+        # KV splits merged by the combine launch) for three of its tokens, every head
+        if p0 > 0:
+            q = g.capture(0, 3, mb * nh * hd).reshape(mb, nh, hd)
+            att = g.capture(0, 2, mb * nh * hd).reshape(mb, nh, hd)
+            cache = _cache_f64(g, kv, nkv, n_ctx, hd)
+            for t in (0, mb // 2, mb - 1):
+                for hq in range(nh):
+                    ref, bound = _attention_f64(oracle, kv, q[t, hq], cache, hq // (nh // nkv), p0 + t + 1)
+                    err = float(np.abs(att[t, hq] - ref).max())
+                    worst_prompt = max(worst_prompt, err / bound)
+                    assert err <= bound, f"kv{kv} prompt position {p0 + t} head {hq}: {err} > {bound}"
     g.set_capture(True)
-    G = nh // nkv
     worst = 0.0
     for p in range(n_prompt, n_prompt + 3):
         g.forward([prompt[p]], p)
         q = g.capture(0, 3, nh * hd).reshape(nh, hd)
         att = g.capture(0, 2, nh * hd).reshape(nh, hd)
-        kr, ks = g.kv_layer(0, 0, nkv, n_ctx)
-        vr, vs = g.kv_layer(0, 1, nkv, n_ctx)
-        n = p + 1
+        cache = _cache_f64(g, kv, nkv, n_ctx, hd)
         for hq in range(nh):
-            h = hq // G
-            if kv == 0:
-                K = kr[h, :n].view(np.float16).astype(np.float64).reshape(n, hd)
-                V = vr[h, :n].view(np.float16).astype(np.float64).reshape(n, hd)
-                s = K @ q[hq].astype(np.float64)
-                w = np.exp(s - s.max())
-                ref = (w / w.sum()) @ V
-                bound = (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * np.abs(V).max() + 1e-6
-            else:
-                kc, ksc = _turbo_rows(kr[h, :n], ks[h, :n], hd)
-                vc, vsc = _turbo_rows(vr[h, :n], vs[h, :n], hd)
-                qa = oracle.quantize_q8_0(oracle.turbo_rotate(q[hq]))  # [hd/32] blocks: qs[32], d
-                qs = qa["qs"].reshape(-1).astype(np.float64)
-                dq = qa["d"].astype(np.float64)
-                idots = (LEVELS_I8[kc] * qs).reshape(n, hd // 32, 32).sum(axis=2)  # exact integers per chunk
-                s = (idots * dq).sum(axis=1) * ksc / 46.0
-                w = np.exp(s - s.max())
-                orot = ((w / w.sum() * vsc)[:, None] * LEVELS_I8[vc] / 46.0).sum(axis=0)
-                ref = oracle.turbo_rotate(orot.astype(np.float32), inverse=True).astype(np.float64)
-                vmax = np.abs(vsc[:, None] * LEVELS_I8[vc] / 46.0).max()
-                bound = (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * vmax + 2e-6 * vmax + 1e-6
+            ref, bound = _attention_f64(oracle, kv, q[hq], cache, hq // (nh // nkv), p + 1)
             err = float(np.abs(att[hq] - ref).max())
             worst = max(worst, err / bound)
             assert err <= bound, f"kv{kv} position {p} head {hq}: {err} > {bound}"
     _record({"config": "llama8b_32k_1layer", "kv": ["f16", "q8_0", "turbo4"][kv], "context": n_prompt + 3,
-             "decode_attention_err_over_bound": worst})
+             "decode_attention_err_over_bound": worst, "prompt_attention_err_over_bound": worst_prompt})
     g.close()
+
+
+def _cache_f64(g, kv, nkv, n_ctx, hd):
+    """The layer-0 cache as the reference reads it: f16 rows as float64, or the
+    Turbo4 rows' codes and scales."""
+    kr, ks = g.kv_layer(0, 0, nkv, n_ctx)
+    vr, vs = g.kv_layer(0, 1, nkv, n_ctx)
+    if kv == 0:
+        return [(kr[h].view(np.float16).astype(np.float64).reshape(-1, hd), vr[h].view(np.float16).astype(np.float64).reshape(-1, hd))
+                for h in range(nkv)]
+    return [(_turbo_rows(kr[h], ks[h], hd), _turbo_rows(vr[h], vs[h], hd)) for h in range(nkv)]
+
+
+def _attention_f64(oracle, kv, q, cache, h, n):
+    """Attention of one prepared query over positions 0..n-1 of KV head h in
+    float64, and the f32 error bound the GPU's output is held to (cpu.rs:550-634;
+    Turbo4: the query rotated and quantized to Q8_0 as cpu.rs:584-600 prepares it,
+    integer level dots per 32-value chunk, dot_rotated_4 turbo.rs:178-193, then the
+    weighted sum of levels and the inverse rotation, turbo.rs:222-250)."""
+    if kv == 0:
+        K, V = cache[h][0][:n], cache[h][1][:n]
+        s = K @ q.astype(np.float64)
+        w = np.exp(s - s.max())
+        ref = (w / w.sum()) @ V
+        return ref, (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * np.abs(V).max() + 1e-6
+    (kc, ksc), (vc, vsc) = cache[h]
+    kc, ksc, vc, vsc = kc[:n], ksc[:n], vc[:n], vsc[:n]
+    hd = kc.shape[1]
+    qa = oracle.quantize_q8_0(oracle.turbo_rotate(q))  # [hd/32] blocks: qs[32], d
+    qs = qa["qs"].reshape(-1).astype(np.float64)
+    dq = qa["d"].astype(np.float64)
+    idots = (LEVELS_I8[kc] * qs).reshape(n, hd // 32, 32).sum(axis=2)  # exact integers per chunk
+    s = (idots * dq).sum(axis=1) * ksc / 46.0
+    w = np.exp(s - s.max())
+    orot = ((w / w.sum() * vsc)[:, None] * LEVELS_I8[vc] / 46.0).sum(axis=0)
+    ref = oracle.turbo_rotate(orot.astype(np.float32), inverse=True).astype(np.float64)
+    vmax = np.abs(vsc[:, None] * LEVELS_I8[vc] / 46.0).max()
+    return ref, (8 * 2.0 ** -24 * np.abs(s).max() + 5e-6) * vmax + 2e-6 * vmax + 1e-6
 
 
 N_DEEP_PROMPT, N_DEEP_TF = 64, 16
