@@ -261,6 +261,13 @@ class Backend:
         self.model = model
         self.h = lib().or_backend_new(model.h, n_ctx, max_batch, kv, n_threads)
         self.n_vocab = model.cfg["n_vocab"]
+        self._n_ctx, self._max_batch = n_ctx, max_batch
+
+    def n_ctx(self) -> int:
+        return self._n_ctx
+
+    def max_batch(self) -> int:
+        return self._max_batch
 
     def __del__(self):
         if getattr(self, "h", None):

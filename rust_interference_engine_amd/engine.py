@@ -1,5 +1,6 @@
 """Engine-level loops over a Backend, mirroring crates/rie-core/src/engine.rs:
-prefix-reusing ``eval_tokens`` (250-272), ``eval_next`` (384-392), ``bench``
+prefix-reusing ``eval_tokens`` (250-272), ``shift_context`` (363-381),
+``eval_next`` (384-392), the greedy path of ``generate`` (420-530), ``bench``
 (540-564) and greedy argmax (sampler.rs:199-209)."""
 from __future__ import annotations
 
@@ -51,6 +52,44 @@ class Engine:
             self.cached.extend(tokens[pos:end])
             pos = end
         return common
+
+    def shift_context(self, n_keep: int, bos: int | None = None) -> bool:
+        """Engine::shift_context: keep the first n_keep cached tokens (at least a
+        leading BOS), drop half of the rest, and evaluate the remainder again at its
+        new positions (its K/V carry the RoPE of the old ones); the kept prefix is
+        reused.  False when nothing can be dropped."""
+        n = len(self.cached)
+        lead_bos = int(bos is not None and n > 0 and self.cached[0] == bos)
+        keep = min(max(n_keep, lead_bos), n)
+        discard = (n - keep) // 2
+        if discard == 0:
+            return False
+        toks = self.cached[:keep] + self.cached[keep + discard:]
+        del self.cached[keep:]
+        self.eval_tokens(toks)
+        return True
+
+    def generate(self, tokens, max_tokens: int, context_shift: bool = True, n_keep: int = 0, bos: int | None = None,
+                 stop_ids=()):
+        """The greedy path of Engine::generate_hooked without text handling: each
+        step takes the argmax of the logits and counts it; a stop id ends the run
+        unevaluated, a full window is shifted (or ends the run when shifting is off
+        or frees nothing), and otherwise the token is evaluated.  Returns the tokens
+        produced, the stop reason ("max_tokens", "end_of_sequence" or
+        "context_full") and the number of prompt tokens reused from the cache."""
+        reused = self.eval_tokens(tokens)
+        out, stop = [], "max_tokens"
+        while len(out) < max_tokens:
+            tok = argmax(self._logits)
+            out.append(tok)
+            if tok in stop_ids:
+                stop = "end_of_sequence"
+                break
+            if len(self.cached) >= self.backend.n_ctx() and (not context_shift or not self.shift_context(n_keep, bos)):
+                stop = "context_full"
+                break
+            self.eval_next(tok)
+        return out, stop, reused
 
     def eval_next(self, token: int) -> None:
         pos = len(self.cached)
