@@ -214,7 +214,8 @@ constexpr int QK_PRO_MAX = 8192;  // widest activation the quantize-only Q8_K pr
 // Q8_K(x), widths up to QK_PRO_MAX.
 template <int TY, int LPR, int UPL, bool GLU, int R, int NT, bool PRO8, bool PROQ = false>
 __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
-    static_assert(!PRO8 || TY == T_Q4_0 || TY == T_Q8_0, "the Q8_0 prologue serves Q4_0/Q8_0 weights");
+    constexpr bool KQ = TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K;
+    static_assert(!PRO8 || TY == T_Q4_0 || TY == T_Q8_0 || KQ, "the norm prologue serves Q4_0/Q8_0 (Q8_0) and K-quant (Q8_K) weights");
     static_assert(!PROQ || ((TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K) && !GLU),
                   "the quantize-only prologue serves K-quant weights");
     constexpr int GROUPS = NT / LPR;
@@ -288,7 +289,7 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
     // the loads in program order waits with it: with every wave's weight loads
     // ahead of the prologue, the activation was ready 8 µs (median) into the
     // gate/up launch, against ~2 µs for the x loads alone.
-    constexpr bool SPLIT = PRO8 && NT >= 512;
+    constexpr bool SPLIT = PRO8 && !KQ && NT >= 512;
     constexpr bool ROUTER = TY == T_F32 && !GLU;  // may carry the MoE routing (p.route)
     __shared__ int s_arrive;  // SPLIT: arrivals of waves 0-3 (4: norm sums, 8: activation)
     if constexpr (SPLIT) {
@@ -296,13 +297,20 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
         lds_barrier();  // at entry, before any load
     }
     float4 xv[4], gv[4];  // values 16τ..16τ+15 of x and of the norm weight
+    float4 kx[4];         // K-quant norm: x at 4τ + 1024k (the standalone Q8_K quantizer's sum order)
     if constexpr (PRO8) {
+        const float *xr = p.nin.x + ((KQ && p.xsel && p.act_per_slot) ? (size_t)slot * p.K : 0);
 #pragma unroll
         for (int i = 0; i < 4; i++) xv[i] = gv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (KQ) {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                kx[k] = (tid < 256 && 4 * tid + 1024 * k < p.K) ? *(const float4 *)(xr + 4 * tid + 1024 * k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
         if (tid < (p.K >> 4)) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                xv[i] = ((const float4 *)(p.nin.x + 16 * tid))[i];
+                xv[i] = ((const float4 *)(xr + 16 * tid))[i];
                 gv[i] = ((const float4 *)(p.nin.w + 16 * tid))[i];
             }
         }
@@ -350,7 +358,52 @@ __device__ __forceinline__ void dec_body(const DecP &p, const int bid) {
         if (base0 < p.tr) load_pass(base0);  // in flight while the activation is prepared
     }
     bool have_act = false;
-    if constexpr (PRO8) {
+    if constexpr (PRO8 && KQ) {
+        // The activation is Q8_K(RMSNorm(x)·w), made here once per workgroup from the
+        // loads issued ahead of the weight stream, with the standalone quantizer's
+        // arithmetic (quant/mod.rs:191-218): the norm's partial sums in rms_scale_wg's
+        // order (the first 256 threads, float4 at 4τ + 1024k; a missing k adds an
+        // exact zero), then 16 threads per superblock (q8k_group_to_lds).  The
+        // barriers order LDS only, so no wave waits for its weight loads here.
+        __shared__ __align__(16) int8_t s_q[4096];
+        __shared__ float s_d[16], s_red[4];
+        __shared__ __align__(16) int16_t s_bs[256];
+        const int K = p.K;
+        float ss = 0.0f;
+        if (tid < 256) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                ss = fmaf(kx[k].x, kx[k].x, ss);
+                ss = fmaf(kx[k].y, kx[k].y, ss);
+                ss = fmaf(kx[k].z, kx[k].z, ss);
+                ss = fmaf(kx[k].w, kx[k].w, ss);
+            }
+        }
+        ss = wave_sum(ss, 64);
+        if ((tid & 63) == 0 && tid < 256) s_red[tid >> 6] = ss;
+        lds_barrier();
+        const float scale = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + p.nin.eps);
+        if (tid < (K >> 4)) {  // whole 16-lane rows
+            float y[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                y[4 * i] = xv[i].x * scale * gv[i].x;
+                y[4 * i + 1] = xv[i].y * scale * gv[i].y;
+                y[4 * i + 2] = xv[i].z * scale * gv[i].z;
+                y[4 * i + 3] = xv[i].w * scale * gv[i].w;
+            }
+            q8k_group_to_lds(y, tid, s_q, s_bs, s_d);
+        }
+        lds_barrier();
+        ActQ8 la;
+        la.qs = s_q;
+        la.d = s_d;
+        la.bsums = s_bs;
+#pragma unroll
+        for (int k = 0; k < UPL; k++)
+            if (valid[k]) load_act<TY>(a[k], uu[k], la, nullptr, K, 0);
+        have_act = true;
+    } else if constexpr (PRO8) {
         {
             // The activation is Q8_0(RMSNorm(x)·w), made here once per workgroup:
             // thread τ normalizes values 16τ..16τ+15 (a 32-block is a thread pair)
@@ -694,10 +747,10 @@ __global__ __launch_bounds__(NT, NT == 512 ? 4 : 1) void gemv_dec_kernel(DecP p)
 // layer): the first n1 workgroups run the Q4_K rows, the others the Q6_K rows.
 // Each half is the single-type kernel's body with its own tile; with a norm input
 // both halves make the Q8_K activation in their prologue.
-template <int L1, int L2>
+template <int L1, int L2, bool PRO = false>
 __global__ __launch_bounds__(256) void gemv_dec_k46_kernel(DecP p1, DecP p2, int n1) {
-    if ((int)blockIdx.x < n1) dec_body<T_Q4_K, L1, 1, false, dec_rows_per_pass<T_Q4_K>(), 256, false>(p1, blockIdx.x);
-    else dec_body<T_Q6_K, L2, 1, false, dec_rows_per_pass<T_Q6_K>(), 256, false>(p2, blockIdx.x - n1);
+    if ((int)blockIdx.x < n1) dec_body<T_Q4_K, L1, 1, false, dec_rows_per_pass<T_Q4_K>(), 256, PRO>(p1, blockIdx.x);
+    else dec_body<T_Q6_K, L2, 1, false, dec_rows_per_pass<T_Q6_K>(), 256, PRO>(p2, blockIdx.x - n1);
 }
 
 static int dec_units(int ty, int K) {
@@ -758,6 +811,7 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
     constexpr bool Q8PRO = TY == T_Q4_0 || TY == T_Q8_0;
     constexpr bool KPRO = TY == T_Q2_K || TY == T_Q3_K || TY == T_Q4_K || TY == T_Q5_K || TY == T_Q6_K;
     const bool pro = Q8PRO && p.nin.x;
+    const bool prok = KPRO && p.nin.x && p.nin.w && p.K <= 4096 && nt == 256;  // RMSNorm + Q8_K in the prologue
     const bool proq = KPRO && p.nin.x && !p.nin.w && !p.glu && nt == 256 && upl == 1 && lpr >= 32 && p.K <= QK_PRO_MAX;
 #define RIE_DEC_P(L, UP, PR)                                                                                          \
     do {                                                                                                              \
@@ -766,13 +820,22 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
         else if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);      \
         else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, PR>), dim3(blocks), dim3(256), lds, st, p);                \
     } while (0)
+#define RIE_DEC_PK(L, UP)                                                                                               \
+    do {                                                                                                                \
+        if (p.glu) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, true, R, 256, true>), dim3(blocks), dim3(256), lds, st, p);   \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, true>), dim3(blocks), dim3(256), lds, st, p);        \
+    } while (0)
 #define RIE_DEC(L, UP)                                                                                                  \
     do {                                                                                                                \
         if constexpr (Q8PRO) {                                                                                          \
             if (pro) RIE_DEC_P(L, UP, true);                                                                            \
             else RIE_DEC_P(L, UP, false);                                                                               \
         } else if constexpr (KPRO && UP == 1 && L >= 32) {                                                              \
-            if (proq) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, 1, false, R, 256, false, true>), dim3(blocks), dim3(256), lds, st, p); \
+            if (prok) RIE_DEC_PK(L, UP);                                                                                \
+            else if (proq) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, 1, false, R, 256, false, true>), dim3(blocks), dim3(256), lds, st, p); \
+            else RIE_DEC_P(L, UP, false);                                                                               \
+        } else if constexpr (KPRO) {                                                                                    \
+            if (prok) RIE_DEC_PK(L, UP);                                                                                \
             else RIE_DEC_P(L, UP, false);                                                                               \
         } else {                                                                                                        \
             RIE_DEC_P(L, UP, false);                                                                                    \
@@ -791,6 +854,7 @@ static bool launch_dec_r(DecP p, hipStream_t st) {
     }
 #undef RIE_DEC
 #undef RIE_DEC_P
+#undef RIE_DEC_PK
     return true;
 }
 
@@ -804,12 +868,20 @@ static bool launch_dec_k46(DecP p1, DecP p2, hipStream_t st) {
     if (u1 != 1 || u2 != 1 || n1t != 256 || n2t != 256 || l2 != 2 * l1) return false;
     const size_t lds = std::max(lds1, lds2);
     const dim3 grid(b1 + b2), block(256);
+    // with a norm input both halves make RMSNorm + Q8_K in the early-load prologue
+    const bool pro = p1.nin.x && p1.nin.w && p2.nin.x && p2.nin.w && p1.K <= 4096;
+#define RIE_K46(A, B)                                                                                            \
+    do {                                                                                                         \
+        if (pro) hipLaunchKernelGGL((gemv_dec_k46_kernel<A, B, true>), grid, block, lds, st, p1, p2, b1);        \
+        else hipLaunchKernelGGL((gemv_dec_k46_kernel<A, B, false>), grid, block, lds, st, p1, p2, b1);           \
+    } while (0)
     switch (l1) {
-    case 32: hipLaunchKernelGGL((gemv_dec_k46_kernel<32, 64>), grid, block, lds, st, p1, p2, b1); return true;
-    case 64: hipLaunchKernelGGL((gemv_dec_k46_kernel<64, 128>), grid, block, lds, st, p1, p2, b1); return true;
-    case 128: hipLaunchKernelGGL((gemv_dec_k46_kernel<128, 256>), grid, block, lds, st, p1, p2, b1); return true;
+    case 32: RIE_K46(32, 64); return true;
+    case 64: RIE_K46(64, 128); return true;
+    case 128: RIE_K46(128, 256); return true;
     default: return false;
     }
+#undef RIE_K46
 }
 
 template <int TY>
