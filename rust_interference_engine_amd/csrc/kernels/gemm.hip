@@ -7,11 +7,13 @@
 //   S[t][r]  = d_a[t][b]·d_w[r][b]                v_mfma_f32_32x32x1f32 (outer product;
 //                                                  two blocks' S per instruction)
 //   acc      = fma((float)I, S, acc)              VALU
+// (Q4_0 codes enter the MFMA as 16·(w_q − 8) and d_w as d_w/16: the same I·S)
 // so each block contributes (d_w·d_a)·isum exactly as the reference's block dot
 // does; only the order of the f32 sum over blocks differs.  Weights stay in
 // their ggml layout: a lane loads its row's 2-block unit (36 / 68 bytes, dword
 // aligned) per stage and writes its codes to LDS as int8, for Q4_0 with the
-// nibbles unpacked and 8 subtracted bytewise (once per workgroup, not per wave).
+// nibbles unpacked to 16·(q − 8) and the 1/16 on the block scale (once per
+// workgroup, not per wave).
 //
 // Operand lane layout (checked by the parity tests): lane l supplies row
 // (l mod 32) and values 16·(l/32)..+16 of the block, for A (tokens) and B
@@ -97,7 +99,7 @@ constexpr int G_AST = G_KC * 32 + 16;  // activation row stride in LDS (bytes, p
 
 template <int TY>
 struct GemmLds {
-    static constexpr int QB = 32;                       // weight codes per block in LDS: int8 (Q4_0 unpacked, −8 applied)
+    static constexpr int QB = 32;                       // weight codes per block in LDS: int8 (Q4_0 unpacked as 16·(q − 8))
     static constexpr int WST = G_KC * QB + 16;          // weight row stride (bytes, padded)
 };
 
@@ -160,22 +162,28 @@ __device__ __forceinline__ void stage_store(GemmStage<TY, GLU, BN> &S, int tid, 
         uint8_t *wq = S.wq[nw] + row * WST + 2 * u * QB;
         float *dw = S.dw[nw] + row * G_KC + 2 * u;
         if constexpr (TY == T_Q4_0) {
-            // nibbles → int8 q − 8 once per workgroup: bytes 0..15 of a block are
-            // values 0..15 (low nibbles), bytes 16..31 values 16..31 (high nibbles)
+            // nibbles → int8 16·(q − 8) once per workgroup: bytes 0..15 of a block are
+            // values 0..15 (low nibbles), bytes 16..31 values 16..31 (high nibbles).
+            // q ^ 8 is q − 8 as a 4-bit two's complement number, so with every nibble
+            // flipped by one XOR, a nibble moved into (or left in) the high half of its
+            // byte, low half zero, is the int8 16·(q − 8): 4 instructions per 8 codes.
+            // The block's product is then 16·I exactly (|16·I| < 2²⁴) and its weight
+            // scale carries the 1/16 (a power of two: d_a·d_w/16 and the fma with 16·I
+            // round exactly as d_a·d_w and I do).
             uint32_t q[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(R.w.w[i + 1], R.w.w[i], 2);
+            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(R.w.w[i + 1], R.w.w[i], 2) ^ 0x88888888u;
 #pragma unroll
-            for (int i = 0; i < 4; i++) q[4 + i] = R.w.w[5 + i];
-            auto lo8 = [](uint32_t v) { return ((v & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u; };
-            auto hi8 = [](uint32_t v) { return (((v >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u; };
+            for (int i = 0; i < 4; i++) q[4 + i] = R.w.w[5 + i] ^ 0x88888888u;
+            auto lo16 = [](uint32_t v) { return (v << 4) & 0xF0F0F0F0u; };
+            auto hi16 = [](uint32_t v) { return v & 0xF0F0F0F0u; };
 #pragma unroll
             for (int b = 0; b < 2; b++) {
-                *(uint4 *)(wq + 32 * b) = make_uint4(lo8(q[4 * b]), lo8(q[4 * b + 1]), lo8(q[4 * b + 2]), lo8(q[4 * b + 3]));
-                *(uint4 *)(wq + 32 * b + 16) = make_uint4(hi8(q[4 * b]), hi8(q[4 * b + 1]), hi8(q[4 * b + 2]), hi8(q[4 * b + 3]));
+                *(uint4 *)(wq + 32 * b) = make_uint4(lo16(q[4 * b]), lo16(q[4 * b + 1]), lo16(q[4 * b + 2]), lo16(q[4 * b + 3]));
+                *(uint4 *)(wq + 32 * b + 16) = make_uint4(hi16(q[4 * b]), hi16(q[4 * b + 1]), hi16(q[4 * b + 2]), hi16(q[4 * b + 3]));
             }
-            dw[0] = h2f(R.w.w[0] & 0xffff);
-            dw[1] = h2f(R.w.w[4] >> 16);
+            dw[0] = h2f(R.w.w[0] & 0xffff) * 0.0625f;
+            dw[1] = h2f(R.w.w[4] >> 16) * 0.0625f;
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) ((uint32_t *)wq)[i] = __builtin_amdgcn_alignbyte(R.w.w[i + 1], R.w.w[i], 2);
