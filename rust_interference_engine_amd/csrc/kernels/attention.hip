@@ -1007,6 +1007,72 @@ __device__ void combine_group(const AttnArgs &a, int h0, float *o_s, float *wts,
     att_finish<HD, G, 256>(a, h0, o_s);
 }
 
+// The same merge for a compile-time range count NS: a thread takes output pairs
+// (d, d + 1), one 64-bit agent-scope load per range brings both partial values, and
+// every range's load of a batch (at most 64 in flight per thread) is issued before
+// the range weights are formed, so a merge over 64 ranges waits for one round trip
+// to the coherence point instead of one per 16 ranges.  The sums run over the
+// ranges in the same order as combine_group's, with the same weights.
+template <int HD, int G, int NS>
+__device__ void combine_group_ns(const AttnArgs &a, int h0, float *o_s, float *wts, float *Ls) {
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    static_assert(NS <= 64 && HD % 2 == 0, "one lane per range in the weight pass; pairs of outputs");
+    constexpr int hd = HD;
+    constexpr size_t prow = (size_t)hd + 2;  // even: every pair (d, d + 1) is 8-byte aligned
+    const float *part0 = a.part + (size_t)h0 * NS * prow;
+    constexpr int NPAIR = G * hd / 2;
+    constexpr int PT = (NPAIR + 255) / 256;                      // pairs per thread
+    constexpr int CP = PT * NS <= 64 ? PT : (NS >= 64 ? 1 : 64 / NS);  // pairs per batch of loads
+    constexpr int NB = (PT + CP - 1) / CP;
+    uint64_t v[CP][NS];
+    auto issue = [&](int bt) {
+#pragma unroll
+        for (int c = 0; c < CP; c++) {
+            const int i = 2 * min(tid + 256 * (bt * CP + c), NPAIR - 1);
+            const float *src = part0 + (size_t)(i / hd) * NS * prow + i % hd;
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+                v[c][s] = __hip_atomic_load((const uint64_t *)(src + (size_t)s * prow), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    issue(0);
+    for (int j = wv; j < G; j += 4) {  // range weights, one wave per head, while the partials are in flight
+        const float *part = part0 + (size_t)j * NS * prow;
+        float mv = -INFINITY, lv = 0.0f;
+        if (lane < NS) {
+            mv = ld_coh(part + (size_t)lane * prow + hd);
+            lv = ld_coh(part + (size_t)lane * prow + hd + 1);
+        }
+        const float m = wave_max(mv, 64);
+        const float w = (lane < NS && lv > 0.0f) ? exp2_hw(mv - m) : 0.0f;
+        if (lane < NS) wts[j * ATT_MAX_SPLIT + lane] = w;
+        const float L = wave_sum(lane < NS ? lv * w : 0.0f, 64);
+        if (lane == 0) Ls[j] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int bt = 0; bt < NB; bt++) {
+        if (bt) issue(bt);
+#pragma unroll
+        for (int c = 0; c < CP; c++) {
+            const int pi = tid + 256 * (bt * CP + c);
+            const int i = 2 * min(pi, NPAIR - 1), j = i / hd;
+            const float *w = wts + j * ATT_MAX_SPLIT;
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                acc0 = fmaf(__uint_as_float((uint32_t)v[c][s]), w[s], acc0);
+                acc1 = fmaf(__uint_as_float((uint32_t)(v[c][s] >> 32)), w[s], acc1);
+            }
+            if (pi < NPAIR) {
+                o_s[i] = acc0 * (1.0f / Ls[j]);
+                o_s[i + 1] = acc1 * (1.0f / Ls[j]);
+            }
+        }
+    }
+    __syncthreads();
+    att_finish<HD, G, 256>(a, h0, o_s);
+}
 
 // G query heads share a KV head; a workgroup takes H of them (H divides G), so the
 // grid is (n_split, n_kv · G / H): blockIdx.y = g · (G / H) + the head slice.
@@ -1276,7 +1342,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, HeadPrepAr
     }
     __syncthreads();
     if (!s_last) return;
-    combine_group<HD, H>(a, h0, qs_f, wo_s[0], wm_s[0]);
+    switch (ns) {  // the decode's range counts (powers of two, 4..64)
+    case 4: combine_group_ns<HD, H, 4>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    case 8: combine_group_ns<HD, H, 8>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    case 16: combine_group_ns<HD, H, 16>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    case 32: combine_group_ns<HD, H, 32>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    case 64: combine_group_ns<HD, H, 64>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    default: combine_group<HD, H>(a, h0, qs_f, wo_s[0], wm_s[0]); break;
+    }
 }
 
 // Short contexts (attention_splits returns one range): one workgroup of ATT_HEAD_NT
