@@ -884,9 +884,63 @@ static bool launch_dec_k46(DecP p1, DecP p2, hipStream_t st) {
 #undef RIE_K46
 }
 
+// Non-gated dense launches of Q4_0/Q8_0 rows with R rows per lane and pass
+// below the type's default (the same kernel body, smaller workgroup tiles).
+template <int TY, int R>
+static bool launch_dec_small(DecP p, hipStream_t st) {
+    int lpr, upl, nt, blocks;
+    size_t lds;
+    if (!plan_dec<TY, R>(p, lpr, upl, nt, lds, blocks) || nt != 256) return false;
+    const bool pro = p.nin.x != nullptr;
+#define RIE_DS(L, UP)                                                                                                      \
+    do {                                                                                                                   \
+        if (pro) hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, true>), dim3(blocks), dim3(256), lds, st, p);  \
+        else hipLaunchKernelGGL((gemv_dec_kernel<TY, L, UP, false, R, 256, false>), dim3(blocks), dim3(256), lds, st, p);     \
+    } while (0)
+    if (upl == 1) {
+        switch (lpr) {
+        case 16: RIE_DS(16, 1); break;
+        case 32: RIE_DS(32, 1); break;
+        case 64: RIE_DS(64, 1); break;
+        case 128: RIE_DS(128, 1); break;
+        default: RIE_DS(256, 1); break;
+        }
+    } else {
+        RIE_DS(256, 2);
+    }
+#undef RIE_DS
+    return true;
+}
+
+// workgroups of the launch for R rows per pass (0 when that tile does not apply)
+template <int TY, int R>
+static int dec_blocks(DecP p) {
+    int lpr, upl, nt, blocks;
+    size_t lds;
+    return plan_dec<TY, R>(p, lpr, upl, nt, lds, blocks) ? blocks : 0;
+}
+
 template <int TY>
 static bool launch_dec_t(const DecP &p, hipStream_t st) {
-    return launch_dec_r<TY, dec_rows_per_pass<TY>()>(p, st);
+    constexpr int R = dec_rows_per_pass<TY>();
+    if constexpr (TY == T_Q4_0 || TY == T_Q8_0) {
+        // Dense non-gated launches whose default tile leaves CUs without a
+        // workgroup (fewer than 256: wo at hidden 2048 has 64 workgroups of 32
+        // rows) take the largest smaller tile that reaches 256 workgroups, or the
+        // smallest.  (A smaller tile only to even out the CUs' loads, e.g. Q/K/V at
+        // hidden 4096 as 768 workgroups instead of 384, measured slower.)
+        if (!p.glu && !p.xsel && !p.route.cnt) {
+            const int b0 = dec_blocks<TY, R>(p);
+            if (b0 > 0 && b0 < 256) {
+                const int b1 = dec_blocks<TY, R / 2>(p);
+                if constexpr (R >= 4) {
+                    if (b1 > 0 && b1 < 256 && dec_blocks<TY, R / 4>(p) > b1 && launch_dec_small<TY, R / 4>(p, st)) return true;
+                }
+                if (b1 > b0 && launch_dec_small<TY, R / 2>(p, st)) return true;
+            }
+        }
+    }
+    return launch_dec_r<TY, R>(p, st);
 }
 
 static bool dispatch_dec(int ty, const DecP &p, hipStream_t st) {
