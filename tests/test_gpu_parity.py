@@ -439,6 +439,33 @@ ATTN_SHAPES = [  # (head_dim, n_head, n_head_kv): lanes per cache row 4/8/16/32,
 ]
 
 
+@pytest.mark.parametrize("kv", [0, 2])
+@pytest.mark.parametrize("n,forced", [(200, True), (1100, False)])
+def test_decode_attention_range_counts(oracle, cuda, n, forced, kv):
+    """The single-token range merge is compiled per range count: 4 ranges (200
+    cached positions, split on request) and 32 (1100 positions), besides the 8, 16
+    and 64 the other tests reach; 4 query heads of 128 per KV head.  Decode logits
+    against the oracle after a prefill in 64-token batches."""
+    from naive_model import max_rel_err
+
+    def mut(s):
+        s.head_dim, s.n_head, s.n_head_kv, s.rope_dim = 128, 8, 2, 128
+    spec, g, o = _pair(oracle, "llama", Q8_0, kv, n_ctx=n + 8, max_batch=64, mutate=mut)
+    nv = spec.n_vocab
+    toks = [(i * 53 + 11) % nv for i in range(n)]
+    pos = 0
+    while pos < n - 3:
+        end = min(pos + 64, n - 3)
+        g.forward(toks[pos:end], pos)
+        o.forward(toks[pos:end], pos)
+        pos = end
+    g.set_attention_ranges(forced)
+    tol = 0.03 if kv == 0 else 0.06
+    for t in range(n - 3, n):
+        err = max_rel_err(g.forward([toks[t]], t), o.forward([toks[t]], t))
+        assert err < tol, f"kv{kv}: {n} positions: decode token {t}: {err}"
+
+
 @pytest.mark.parametrize("kv", [0, 1, 2])
 @pytest.mark.parametrize("hd,nh,nkv", ATTN_SHAPES)
 def test_attention_shapes_match_oracle(oracle, cuda, hd, nh, nkv, kv):
