@@ -31,7 +31,13 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t h1, uint32_t h2, uint32_t
 // A unit is what one lane loads and dots at a time:
 //   Q4_0/Q4_1/Q5_0/Q5_1/Q8_0 : two 32-value blocks (36/40/44/48/68 bytes, dword aligned when K % 64 == 0)
 //   Q4_K/Q5_K                : a 64-value quarter of a superblock
-//   Q2_K/Q3_K/Q6_K           : a 32-value eighth of a superblock
+//   Q6_K                     : two 32-value pieces of one 128-value half n of a
+//                              superblock, values 128n + 32k + [0, 32) and
+//                              128n + 32k + 64 + [0, 32) (k < 2), the low and high
+//                              nibbles of the same 32 ql bytes and two bit planes of
+//                              the half's 32 qh bytes: a lane's loaded bytes serve
+//                              both pieces
+//   Q2_K/Q3_K                : a 32-value eighth of a superblock
 //   F32/F16/BF16             : 8 values
 template <int TY>
 struct ActSlice {
@@ -76,16 +82,24 @@ __device__ __forceinline__ void load_act(ActSlice<TY> &a, int u, const ActQ8 &ac
 #pragma unroll
         for (int i = 0; i < 4; i++) a.bs[i] = act.bsums[(size_t)t * (K >> 4) + 16 * sb + 4 * qi + i];
     } else if constexpr (TY == T_Q6_K) {
-        const int sb = u >> 3, r = u & 7, n = r >> 2, k = r & 3;
-        const uint4 *ap = (const uint4 *)(act.qs + (size_t)t * K + 256 * sb + 128 * n + 32 * k);
+        // unit (n, k): values 128n + 32k + [0, 32) in q[0..7], +64 in q[8..15]
+        const int sb = u >> 2, n = (u >> 1) & 1, k = u & 1;
+        const int8_t *base = act.qs + (size_t)t * K + 256 * sb + 128 * n + 32 * k;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint4 v = ap[i];
-            a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+        for (int h = 0; h < 2; h++) {
+            const uint4 *ap = (const uint4 *)(base + 64 * h);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint4 v = ap[i];
+                a.q[8 * h + 4 * i] = v.x; a.q[8 * h + 4 * i + 1] = v.y; a.q[8 * h + 4 * i + 2] = v.z; a.q[8 * h + 4 * i + 3] = v.w;
+            }
         }
         a.d0 = act.d[(size_t)t * (K >> 8) + sb];
-        a.bs[0] = act.bsums[(size_t)t * (K >> 4) + 16 * sb + 8 * n + 2 * k];
-        a.bs[1] = act.bsums[(size_t)t * (K >> 4) + 16 * sb + 8 * n + 2 * k + 1];
+        const size_t bi = (size_t)t * (K >> 4) + 16 * sb + 8 * n + 2 * k;  // the 16-value sums of the two pieces
+        a.bs[0] = act.bsums[bi];
+        a.bs[1] = act.bsums[bi + 1];
+        a.bs[2] = act.bsums[bi + 4];
+        a.bs[3] = act.bsums[bi + 5];
     } else if constexpr (TY == T_Q2_K || TY == T_Q3_K) {
         // unit (n, js) covers values 128n + 32js .. +32 of its superblock
         const int sb = u >> 3, r = u & 7;
@@ -116,7 +130,7 @@ template <> struct Raw<T_Q5_1> { uint32_t w[12]; };
 template <> struct Raw<T_Q8_0> { uint32_t w[17]; };
 template <> struct Raw<T_Q4_K> { u32x4 hdr, v0, v1; };
 template <> struct Raw<T_Q5_K> { u32x4 hdr, v0, v1, h0, h1; };
-template <> struct Raw<T_Q6_K> { uint32_t ql[9], qh[9], sh_l, sh_h, scw, d; };
+template <> struct Raw<T_Q6_K> { uint32_t ql[9], qh[9], sh_l, sh_h, sc0, sc1, d; };
 template <> struct Raw<T_Q2_K> { uint32_t q[8], sc, dd; };
 template <> struct Raw<T_Q3_K> { uint32_t q[9], hm[9], s[4], dd, sh; };
 template <> struct Raw<T_F32> { f32x4 a, b; };
@@ -125,7 +139,7 @@ template <> struct Raw<T_BF16> { u32x4 a; };
 
 template <int TY>
 __device__ __forceinline__ int units_per_row(int K) {
-    if (TY == T_Q6_K || TY == T_Q2_K || TY == T_Q3_K) return K >> 5;
+    if (TY == T_Q2_K || TY == T_Q3_K) return K >> 5;
     if (TY == T_F32 || TY == T_F16 || TY == T_BF16) return K >> 3;
     return K >> 6;
 }
@@ -162,9 +176,9 @@ __device__ __forceinline__ void load_raw(const uint8_t *__restrict__ row, int u,
         r.v0 = wload((const u32x4 *)(b + 48 + 32 * qi));
         r.v1 = wload((const u32x4 *)(b + 64 + 32 * qi));
     } else if constexpr (TY == T_Q6_K) {
-        const int sb = u >> 3, rr = u & 7, n = rr >> 2, k = rr & 3;
+        const int sb = u >> 2, n = (u >> 1) & 1, k = u & 1;
         const uint8_t *b = row + 210 * sb;
-        const uintptr_t al = (uintptr_t)(b + 64 * n + 32 * (k & 1)), ah = (uintptr_t)(b + 128 + 32 * n);
+        const uintptr_t al = (uintptr_t)(b + 64 * n + 32 * k), ah = (uintptr_t)(b + 128 + 32 * n);
         const uint32_t *ql = (const uint32_t *)(al & ~(uintptr_t)3), *qh = (const uint32_t *)(ah & ~(uintptr_t)3);
 #pragma unroll
         for (int i = 0; i < 9; i++) {
@@ -173,7 +187,8 @@ __device__ __forceinline__ void load_raw(const uint8_t *__restrict__ row, int u,
         }
         r.sh_l = (uint32_t)(al & 3);
         r.sh_h = (uint32_t)(ah & 3);
-        r.scw = wload((const uint16_t *)(b + 192 + 8 * n + 2 * k));
+        r.sc0 = wload((const uint16_t *)(b + 192 + 8 * n + 2 * k));      // scales of the first piece's 16-value halves
+        r.sc1 = wload((const uint16_t *)(b + 192 + 8 * n + 2 * k + 4));  // and of the second piece's
         r.d = wload((const uint16_t *)(b + 208));
     } else if constexpr (TY == T_Q2_K) {
         // 84-byte superblocks: scales[16] | q[64] | d | dmin (dword aligned when K % 512 == 0 or the row starts so)
@@ -331,18 +346,26 @@ __device__ __forceinline__ float dot_raw(const Raw<TY> &r, int u, const ActSlice
         const int summ = mn[0] * ((int)a.bs[0] + a.bs[1]) + mn[1] * ((int)a.bs[2] + a.bs[3]);
         return (h2f(r.hdr.x & 0xffff) * a.d0) * (float)sumi - (h2f(r.hdr.x >> 16) * a.d0) * (float)summ;
     } else if constexpr (TY == T_Q6_K) {
-        const int k = u & 3;
-        const int sh = k >= 2 ? 4 : 0, hs = 2 * k;
-        int dl = 0, dh = 0;
+        // piece 0: low nibbles and qh bits 2k, 2k+1; piece 1: high nibbles and bits
+        // 2k+4, 2k+5 (q6 = nibble | 2 bits << 4, value q6 − 32: reference.rs:352-385)
+        const int hs = 2 * (u & 1);
+        int d0l = 0, d0h = 0, d1l = 0, d1h = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const uint32_t ql = __builtin_amdgcn_alignbyte(r.ql[j + 1], r.ql[j], r.sh_l);
             const uint32_t qh = __builtin_amdgcn_alignbyte(r.qh[j + 1], r.qh[j], r.sh_h);
-            const uint32_t v = ((ql >> sh) & M4) | (((qh >> hs) & 0x03030303u) << 4);
-            if (j < 4) dl = sdot4(v, a.q[j], dl);
-            else dh = sdot4(v, a.q[j], dh);
+            const uint32_t v0 = (ql & M4) | (((qh >> hs) & 0x03030303u) << 4);
+            const uint32_t v1 = ((ql >> 4) & M4) | (((qh >> (hs + 4)) & 0x03030303u) << 4);
+            if (j < 4) {
+                d0l = sdot4(v0, a.q[j], d0l);
+                d1l = sdot4(v1, a.q[8 + j], d1l);
+            } else {
+                d0h = sdot4(v0, a.q[j], d0h);
+                d1h = sdot4(v1, a.q[8 + j], d1h);
+            }
         }
-        const int sumi = (int)(int8_t)(r.scw & 0xff) * (dl - 32 * a.bs[0]) + (int)(int8_t)(r.scw >> 8) * (dh - 32 * a.bs[1]);
+        const int sumi = (int)(int8_t)(r.sc0 & 0xff) * (d0l - 32 * a.bs[0]) + (int)(int8_t)(r.sc0 >> 8) * (d0h - 32 * a.bs[1]) +
+                         (int)(int8_t)(r.sc1 & 0xff) * (d1l - 32 * a.bs[2]) + (int)(int8_t)(r.sc1 >> 8) * (d1h - 32 * a.bs[3]);
         return h2f(r.d) * a.d0 * (float)sumi;
     } else if constexpr (TY == T_Q2_K) {
         // y = d·(sc & 15)·q − dmin·(sc >> 4) per 16 values (reference.rs:101-125); unit (n, js)

@@ -754,7 +754,7 @@ __global__ __launch_bounds__(256) void gemv_dec_k46_kernel(DecP p1, DecP p2, int
 }
 
 static int dec_units(int ty, int K) {
-    if (ty == T_Q6_K || ty == T_Q2_K || ty == T_Q3_K) return K / 32;
+    if (ty == T_Q2_K || ty == T_Q3_K) return K / 32;
     if (ty == T_F32 || ty == T_F16 || ty == T_BF16) return K / 8;
     return K / 64;
 }
@@ -865,7 +865,7 @@ static bool launch_dec_k46(DecP p1, DecP p2, hipStream_t st) {
     if (!plan_dec<T_Q4_K, dec_rows_per_pass<T_Q4_K>()>(p1, l1, u1, n1t, lds1, b1) ||
         !plan_dec<T_Q6_K, dec_rows_per_pass<T_Q6_K>()>(p2, l2, u2, n2t, lds2, b2))
         return false;
-    if (u1 != 1 || u2 != 1 || n1t != 256 || n2t != 256 || l2 != 2 * l1) return false;
+    if (u1 != 1 || u2 != 1 || n1t != 256 || n2t != 256 || l2 != l1) return false;
     const size_t lds = std::max(lds1, lds2);
     const dim3 grid(b1 + b2), block(256);
     // with a norm input both halves make RMSNorm + Q8_K in the early-load prologue
@@ -876,9 +876,9 @@ static bool launch_dec_k46(DecP p1, DecP p2, hipStream_t st) {
         else hipLaunchKernelGGL((gemv_dec_k46_kernel<A, B, false>), grid, block, lds, st, p1, p2, b1);           \
     } while (0)
     switch (l1) {
-    case 32: RIE_K46(32, 64); return true;
-    case 64: RIE_K46(64, 128); return true;
-    case 128: RIE_K46(128, 256); return true;
+    case 32: RIE_K46(32, 32); return true;
+    case 64: RIE_K46(64, 64); return true;
+    case 128: RIE_K46(128, 128); return true;
     default: return false;
     }
 #undef RIE_K46
