@@ -54,7 +54,7 @@ class Engine:
         return common
 
     def shift_context(self, n_keep: int, bos: int | None = None) -> bool:
-        """Engine::shift_context: keep the first n_keep cached tokens (at least a
+        """Engine::shift_context (crates/rie-core/src/engine.rs:366-382): keep the first n_keep cached tokens (at least a
         leading BOS), drop half of the rest, and evaluate the remainder again at its
         new positions (its K/V carry the RoPE of the old ones); the kept prefix is
         reused.  False when nothing can be dropped."""
@@ -71,7 +71,7 @@ class Engine:
 
     def generate(self, tokens, max_tokens: int, context_shift: bool = True, n_keep: int = 0, bos: int | None = None,
                  stop_ids=()):
-        """The greedy path of Engine::generate_hooked without text handling: each
+        """The greedy path of Engine::generate_hooked (crates/rie-core/src/engine.rs:420-537) without text handling: each
         step takes the argmax of the logits and counts it; a stop id ends the run
         unevaluated, a full window is shifted (or ends the run when shifting is off
         or frees nothing), and otherwise the token is evaluated.  Returns the tokens
