@@ -241,7 +241,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
         d_moe_rows_ = dalloc<int>(allocs_, mb * nu);
         d_moe_rw_ = dalloc<float>(allocs_, mb * nu);
         // device-side grouping of prompt batches (grouped expert GEMMs)
-        moe_max_tiles_ = moe_group_max_tiles((int)mb, (int)nu, (int)c.n_expert);
+        moe_max_tiles_ = moe_group_max_tiles((int)mb, (int)nu, (int)c.n_expert, 32);  // the smaller tiles' bound
         d_moe_off_ = dalloc<int>(allocs_, c.n_expert + 1);
         d_moe_rtok_ = dalloc<int>(allocs_, mb * nu);
         d_moe_rslot_ = dalloc<int>(allocs_, mb * nu);
@@ -702,15 +702,19 @@ bool HipBackend::ffn_moe(const DevLayer &L, int n, bool direct) {
         // token map, hidden rows in gathered order), the hidden's quantization, one for
         // every expert's down projection (rows scattered to their pair slots), and the
         // per-token combine in ascending expert order (cpu.rs:487-513).
-        launch_moe_group(d_moe_sel_, n, k, ne, d_moe_off_, d_moe_rtok_, d_moe_rslot_, d_moe_tile_e_, d_moe_tile_r0_, d_moe_ntiles_, st_);
+        // Q4_K experts: 32-token tiles (128 rows × 32 tokens per workgroup), since a
+        // prompt's experts hold a few dozen rows each; other types: GROUP_BN
+        const int bn = L.gate.ty == T_Q4_K && L.down.ty == T_Q4_K ? 32 : GROUP_BN;
+        launch_moe_group(d_moe_sel_, n, k, ne, d_moe_off_, d_moe_rtok_, d_moe_rslot_, d_moe_tile_e_, d_moe_tile_r0_, d_moe_ntiles_, bn, st_);
         check_launch("moe group");
         GroupTiles g;
+        g.bn = bn;
         g.tile_e = d_moe_tile_e_;
         g.tile_r0 = d_moe_tile_r0_;
         g.n_tiles = d_moe_ntiles_;
         g.off = d_moe_off_;
         g.amap = d_moe_rtok_;
-        g.max_tiles = moe_max_tiles_;
+        g.max_tiles = moe_group_max_tiles(n, k, ne, bn);
         DevWeight ge = L.gate, ue = L.up, de = L.down;  // expert 0's matrices; the others follow at wstride
         ge.rows = ue.rows = (size_t)ff;
         de.rows = (size_t)E;

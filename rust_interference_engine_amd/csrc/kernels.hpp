@@ -161,8 +161,8 @@ bool launch_gemv_glu_experts(const DevWeight &gate, const DevWeight &up, int ff,
 
 // ---- grouped expert GEMMs (prompt batches of MoE layers, moe_ffn cpu.rs:487-524) ----
 // The routed (token, slot) pairs of a batch, grouped by expert on the device: gathered
-// row r of expert e lies in [off[e], off[e+1]); token tiles of GROUP_BN rows list their
-// expert and first row.  A grouped GEMM runs one weight matrix per expert (expert e's at
+// row r of expert e lies in [off[e], off[e+1]); token tiles of bn rows (GROUP_BN, or 32
+// for Q4_K experts) list their expert and first row.  A grouped GEMM runs one weight matrix per expert (expert e's at
 // w + e·wstride) over that expert's rows only; its activation row for gathered row r is
 // amap[r] (or r), its output row omap[r] (or r).
 constexpr int GROUP_BN = 64;
@@ -171,13 +171,14 @@ struct GroupTiles {
     const int *amap = nullptr, *omap = nullptr;
     size_t wstride = 0;
     int max_tiles = 0;  // grid bound: token tiles of the largest possible grouping
+    int bn = GROUP_BN;  // rows per token tile (32: the Q4_K GEMMs' 128 × 32 tiles)
 };
 // sel [n_tok·k] (ascending experts per token) → off [n_exp+1], row_tok / row_slot
 // [n_tok·k] (token t and pair index t·k + j of each gathered row), the tile table
 // (tile_e / tile_r0 [max_tiles], *n_tiles).  One workgroup; n_exp ≤ 512.
 void launch_moe_group(const int *sel, int n_tok, int k, int n_exp, int *off, int *row_tok, int *row_slot, int *tile_e, int *tile_r0,
-                      int *n_tiles, hipStream_t st);
-int moe_group_max_tiles(int n_tok, int k, int n_exp);
+                      int *n_tiles, int bn, hipStream_t st);
+int moe_group_max_tiles(int n_tok, int k, int n_exp, int bn = GROUP_BN);
 
 // ---- gemm_kq.hip (prefill, Q4_K × Q8_K on int8 MFMA; reached through gemm.hip) ----
 bool gemm_kq_supported(int ty, size_t K);

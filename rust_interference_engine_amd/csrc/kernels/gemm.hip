@@ -416,6 +416,7 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
     if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act) || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
     if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st, grp);
+    if (grp && grp->bn != GROUP_BN) return false;  // this kernel's grouped tiles are 64 tokens
     GemmP p{};
     for (int i = 0; i < nseg; i++) {
         const GemvSeg &s = segs[i];
@@ -444,6 +445,7 @@ bool launch_gemm_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &ac
     (void)scratch;
     if (grp && grp->max_tiles < 1) return false;
     if (gemm_kq_supported(gate.ty, K)) return launch_gemm_kq_glu(gate, up, act, n_tok, K, h, ld, gelu, st, grp);
+    if (grp && grp->bn != GROUP_BN) return false;  // this kernel's grouped tiles are 64 tokens
     if (n_tok < 1 || !operands_ok(act) || gate.ty != up.ty || !gemm_supported(gate.ty, K) || gate.cols != (size_t)K ||
         up.cols != (size_t)K || gate.rows != up.rows || !gate.data || !up.data || !h)
         return false;

@@ -31,6 +31,8 @@
 #include "../kernels.hpp"
 #include "../gemv_units.hpp"
 
+#include <type_traits>
+
 namespace rie {
 
 namespace {
@@ -62,6 +64,9 @@ struct KqP {
 
 constexpr int KQ_BM = 64, KQ_BN = 64;
 static_assert(KQ_BN == GROUP_BN, "grouped tiles are built for this token tile");
+// Q4_K tiles of BN = 32 tokens (groupings of Q4_K experts, a few dozen rows each)
+// are 128 weight rows tall: the four waves stand along the rows
+template <int BN> constexpr int kq_bm() { return BN == 64 ? 64 : 128; }
 
 // A workgroup's token rows: tokens [r0, r_end) of the batch, or gathered rows
 // [r0, r_end) of expert e (e < 0: a tile past the grouping's count, nothing to
@@ -69,57 +74,74 @@ static_assert(KQ_BN == GROUP_BN, "grouped tiles are built for this token tile");
 struct TileRows {
     int r0, r_end, e;
 };
+template <int BN = KQ_BN>
 __device__ __forceinline__ TileRows tile_rows(const KqP &p, int tg) {
-    if (!p.grouped) return TileRows{tg * KQ_BN, p.n_tok, 0};
+    if (!p.grouped) return TileRows{tg * BN, p.n_tok, 0};
     if (tg >= *p.grp.n_tiles) return TileRows{0, 0, -1};
     const int e = p.grp.tile_e[tg], r0 = p.grp.tile_r0[tg];
-    return TileRows{r0, min(p.grp.off[e + 1], r0 + KQ_BN), e};
+    return TileRows{r0, min(p.grp.off[e + 1], r0 + BN), e};
 }
 __device__ __forceinline__ int act_row(const KqP &p, int r) { return p.grouped && p.grp.amap ? p.grp.amap[r] : r; }
 __device__ __forceinline__ int out_row(const KqP &p, int r) { return p.grouped && p.grp.omap ? p.grp.omap[r] : r; }
 constexpr int KA_ST = 128 + 16;  // activation bytes per token in LDS (one half superblock, padded)
 constexpr int KW_ST = 64 + 16;   // weight nibble bytes per row in LDS (one half superblock, padded)
 
-template <bool GLU>
+// BN = 32 keeps the 6-bit scales and mins as bytes, so that two 128-row stages of
+// the gated pair fit two workgroups in a CU's LDS.
+template <bool GLU, int BN = KQ_BN>
 struct __align__(16) KqStage {
-    static constexpr int NW = GLU ? 2 : 1;
-    int8_t a[KQ_BN * KA_ST];
-    float da[KQ_BN];
-    float bs[KQ_BN * 8];           // the superblock's 32-value activation sums (both halves hold all 8)
-    uint8_t wq[NW][KQ_BM * KW_ST];
-    float wd[NW][KQ_BM], wdm[NW][KQ_BM];
-    int wsc[NW][KQ_BM * 8];        // 6-bit scales of the 8 sub-blocks
-    float wm[NW][KQ_BM * 8];       // 6-bit mins
+    static constexpr int NW = GLU ? 2 : 1, BM = kq_bm<BN>();
+    using ScT = std::conditional_t<BN == 64, int, uint8_t>;
+    using MnT = std::conditional_t<BN == 64, float, uint8_t>;
+    int8_t a[BN * KA_ST];
+    float da[BN];
+    float bs[BN * 8];              // the superblock's 32-value activation sums (both halves hold all 8)
+    uint8_t wq[NW][BM * KW_ST];
+    float wd[NW][BM], wdm[NW][BM];
+    ScT wsc[NW][BM * 8];           // 6-bit scales of the 8 sub-blocks
+    MnT wm[NW][BM * 8];            // 6-bit mins
 };
 
+template <bool GLU, int BN = KQ_BN>
 struct KqRegs {
-    v4i a[2];         // 32 activation bytes of the thread's token
+    static constexpr int NA = BN == 64 ? 2 : 1, NQ = (BN == 32 && GLU) ? 4 : 2;
+    v4i a[NA];        // 32 (BN 64) or 16 (BN 32) activation bytes of the thread's token
     float da;
     v4i bs[2];        // the token's 16 bsums (int16)
-    v4i wq[2];        // 32 nibble bytes of the thread's row
+    v4i wq[NQ];       // 32 nibble bytes of the thread's row (64, both units, in the 32-token gated form)
     v4i hdr;          // d, dmin, scales[12]
 };
 
 // stage loads for half hs of superblock sb
-// tokA: the activation row of the thread's token (tid/4); tokD: of token tid (tid < 64);
-// woff: the expert's byte offset in a grouped launch
-template <bool GLU>
+// tokA: the activation row of the thread's token (tid/4, or tid/8 for BN 32); tokD: of
+// token tid (tid < BN); woff: the expert's byte offset in a grouped launch
+template <bool GLU, int BN = KQ_BN>
 __device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int tokA, int tokD, size_t woff, int sb, int hs, int tid,
-                                        KqRegs &R) {
+                                        KqRegs<GLU, BN> &R) {
     const int K = p.K, nsb = K >> 8;
-    {
+    if constexpr (BN == 64) {
         const v4i *src = (const v4i *)(p.qs + (size_t)tokA * K + 256 * sb + 128 * hs + 32 * (tid & 3));
         R.a[0] = src[0];
         R.a[1] = src[1];
+    } else {
+        R.a[0] = *(const v4i *)(p.qs + (size_t)tokA * K + 256 * sb + 128 * hs + 16 * (tid & 7));
     }
-    if (tid < KQ_BN) {
+    if (tid < BN) {
         R.da = p.d[(size_t)tokD * nsb + sb];
         const v4i *bsrc = (const v4i *)(p.bsums + (size_t)tokD * (K >> 4) + 16 * sb);
         R.bs[0] = bsrc[0];
         R.bs[1] = bsrc[1];
     }
-    if (GLU || tid < 128) {
-        const int nw = GLU ? (tid >> 7) : 0, idx = tid & 127, u = idx & 1;
+    if constexpr (BN == 32 && GLU) {  // thread → (matrix, row): both units of the half
+        const int nw = tid >> 7;
+        const int row = min(row0 + (tid & 127), p.rows[0] - 1);
+        const uint8_t *blk = p.w[nw] + woff + (size_t)row * p.rb[nw] + 144 * (size_t)sb;
+        const v4i *q = (const v4i *)(blk + 16 + 64 * hs);
+#pragma unroll
+        for (int i = 0; i < 4; i++) R.wq[i] = wload(q + i);
+        R.hdr = wload((const v4i *)blk);
+    } else if (GLU || BN == 32 || tid < 128) {  // thread → (matrix, row, unit)
+        const int nw = (GLU && BN == 64) ? (tid >> 7) : 0, idx = BN == 64 ? (tid & 127) : tid, u = idx & 1;
         const int s = GLU ? nw : sg;
         const int row = min(row0 + (idx >> 1), p.rows[GLU ? 0 : sg] - 1);
         const uint8_t *blk = p.w[s] + woff + (size_t)row * p.rb[s] + 144 * (size_t)sb;
@@ -130,14 +152,16 @@ __device__ __forceinline__ void kq_load(const KqP &p, int sg, int row0, int tokA
     }
 }
 
-template <bool GLU>
-__device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs &R) {
-    {
+template <bool GLU, int BN = KQ_BN>
+__device__ __forceinline__ void kq_store(KqStage<GLU, BN> &S, int tid, const KqRegs<GLU, BN> &R) {
+    if constexpr (BN == 64) {
         v4i *dst = (v4i *)(S.a + (tid >> 2) * KA_ST + 32 * (tid & 3));
         dst[0] = R.a[0];
         dst[1] = R.a[1];
+    } else {
+        *(v4i *)(S.a + (tid >> 3) * KA_ST + 16 * (tid & 7)) = R.a[0];
     }
-    if (tid < KQ_BN) {
+    if (tid < BN) {
         S.da[tid] = R.da;
         const uint32_t w[8] = {(uint32_t)R.bs[0][0], (uint32_t)R.bs[0][1], (uint32_t)R.bs[0][2], (uint32_t)R.bs[0][3],
                                (uint32_t)R.bs[1][0], (uint32_t)R.bs[1][1], (uint32_t)R.bs[1][2], (uint32_t)R.bs[1][3]};
@@ -145,11 +169,24 @@ __device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs 
         for (int j = 0; j < 8; j++)  // bsum_2j + bsum_2j+1 = the two int16 halves of dword j
             S.bs[tid * 8 + j] = (float)((int)(int16_t)(w[j] & 0xffff) + (int)(int16_t)(w[j] >> 16));
     }
-    if (GLU || tid < 128) {
-        const int nw = GLU ? (tid >> 7) : 0, idx = tid & 127, row = idx >> 1, u = idx & 1;
-        v4i *dst = (v4i *)(S.wq[nw] + row * KW_ST + 32 * u);
-        dst[0] = R.wq[0];
-        dst[1] = R.wq[1];
+    if (GLU || BN == 32 || tid < 128) {
+        int nw, row, u;
+        if constexpr (BN == 32 && GLU) {
+            nw = tid >> 7;
+            row = tid & 127;
+            u = 0;
+            v4i *dst = (v4i *)(S.wq[nw] + row * KW_ST);
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[i] = R.wq[i];
+        } else {
+            nw = (GLU && BN == 64) ? (tid >> 7) : 0;
+            const int idx = BN == 64 ? (tid & 127) : tid;
+            row = idx >> 1;
+            u = idx & 1;
+            v4i *dst = (v4i *)(S.wq[nw] + row * KW_ST + 32 * u);
+            dst[0] = R.wq[0];
+            dst[1] = R.wq[1];
+        }
         if (u == 0) {
             const uint32_t h0 = (uint32_t)R.hdr[0], h1 = (uint32_t)R.hdr[1], h2 = (uint32_t)R.hdr[2], h3 = (uint32_t)R.hdr[3];
             S.wd[nw][row] = h2f(h0 & 0xffff);
@@ -158,8 +195,8 @@ __device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs 
             for (int j = 0; j < 8; j++) {
                 int sc, mn;
                 q4k_scale_min(h1, h2, h3, j, sc, mn);  // get_scale_min_k4 (quant/reference.rs:8-16)
-                S.wsc[nw][row * 8 + j] = sc;
-                S.wm[nw][row * 8 + j] = (float)mn;
+                S.wsc[nw][row * 8 + j] = (typename KqStage<GLU, BN>::ScT)sc;
+                S.wm[nw][row * 8 + j] = (typename KqStage<GLU, BN>::MnT)mn;
             }
         }
     }
@@ -172,24 +209,24 @@ __device__ __forceinline__ void kq_store(KqStage<GLU> &S, int tid, const KqRegs 
 // result only for instructions it generates itself.
 __device__ __forceinline__ int mad24(int a, int b, int c) { return c + __mul24(a, b); }
 
-template <bool GLU>
+template <bool GLU, int BN = KQ_BN>
 __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
-    constexpr int NW = GLU ? 2 : 1;
-    __shared__ KqStage<GLU> st[2];
+    constexpr int NW = GLU ? 2 : 1, BM = kq_bm<BN>(), WC = BN / 32;  // waves along the tokens
+    __shared__ KqStage<GLU, BN> st[2];
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-    const int wr = wv >> 1, wc = wv & 1;
+    const int wr = wv / WC, wc = wv % WC;
     const int bid = blockIdx.x;  // workgroups of one row group share an XCD (id mod 8)
     const int xcd = bid & 7, u = bid >> 3;
     const int tg = u % p.n_tg;
     const int rg = (u / p.n_tg) * 8 + xcd;
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
     const int sg = (!GLU && p.nseg > 1 && rg >= p.rg_end[0]) ? ((p.nseg > 2 && rg >= p.rg_end[1]) ? 2 : 1) : 0;
-    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * KQ_BM;
-    const TileRows tr = tile_rows(p, tg);
+    const int row0 = (rg - (sg ? p.rg_end[sg - 1] : 0)) * BM;
+    const TileRows tr = tile_rows<BN>(p, tg);
     if (tr.e < 0) return;  // whole workgroup: uniform
     const size_t woff = p.grouped ? (size_t)tr.e * p.grp.wstride : 0;
-    const int tokA = act_row(p, min(tr.r0 + (tid >> 2), tr.r_end - 1));
-    const int tokD = act_row(p, min(tr.r0 + (tid & 63), tr.r_end - 1));
+    const int tokA = act_row(p, min(tr.r0 + (tid >> (BN == 64 ? 2 : 3)), tr.r_end - 1));
+    const int tokD = act_row(p, min(tr.r0 + (tid & (BN - 1)), tr.r_end - 1));
     const int h = l >> 5, m = l & 31;
     const int tok_m = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int wrow = wr * 32 + m;   // this lane's weight row (B operand / result column)
@@ -208,14 +245,14 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
             s1[a][v] = 0;
         }
     const int n_stages = (p.K >> 8) * 2;
-    KqRegs R;
-    kq_load<GLU>(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
-    kq_store<GLU>(st[0], tid, R);
+    KqRegs<GLU, BN> R;
+    kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
+    kq_store<GLU, BN>(st[0], tid, R);
     __syncthreads();
     for (int s = 0; s < n_stages; s++) {
         const int hs = s & 1;
-        if (s + 1 < n_stages) kq_load<GLU>(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
-        const KqStage<GLU> &S = st[s & 1];
+        if (s + 1 < n_stages) kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        const KqStage<GLU, BN> &S = st[s & 1];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const v4i av = *(const v4i *)(S.a + arow * KA_ST + 32 * j + 16 * h);
@@ -226,7 +263,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
                 const v4i bw = {(int)((q.x >> sh) & 0x0F0F0F0Fu), (int)((q.y >> sh) & 0x0F0F0F0Fu), (int)((q.z >> sh) & 0x0F0F0F0Fu),
                                 (int)((q.w >> sh) & 0x0F0F0F0Fu)};
                 const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, zi, 0, 0, 0);
-                const int sc = S.wsc[a][wrow * 8 + 4 * hs + j];  // |sc| < 64, |I| < 2^16
+                const int sc = (int)S.wsc[a][wrow * 8 + 4 * hs + j];  // |sc| < 64, |I| < 2^16
 #pragma unroll
                 for (int v = 0; v < 16; v++) s1[a][v] = mad24(sc, I[v], s1[a][v]);
             }
@@ -243,7 +280,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
                 for (int q = 0; q < 4; q++) {
                     const int j = 4 * h + q;
                     const int bsj = (int)S.bs[arow * 8 + j];
-                    const float mj = S.wm[a][wrow * 8 + j];
+                    const float mj = (float)S.wm[a][wrow * 8 + j];
                     ab[2 * q] = (_Float16)(float)(bsj & 63);
                     ab[2 * q + 1] = (_Float16)(float)(bsj >> 6);
                     bb[2 * q] = (_Float16)mj;
@@ -260,7 +297,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
                 }
             }
         }
-        if (s + 1 < n_stages) kq_store<GLU>(st[(s + 1) & 1], tid, R);
+        if (s + 1 < n_stages) kq_store<GLU, BN>(st[(s + 1) & 1], tid, R);
         __syncthreads();
     }
     // ---- epilogue: lane holds weight row row0 + wrow for tokens t0 + wc·32 + 16h + v ----
@@ -445,10 +482,10 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     }
 }
 
-void kq_groups(KqP &p, int nseg, const GroupTiles *grp) {
+void kq_groups(KqP &p, int nseg, const GroupTiles *grp, int bm = KQ_BM) {
     int acc = 0;
     for (int i = 0; i < 3; i++) {
-        if (i < nseg) acc += (p.rows[i] + KQ_BM - 1) / KQ_BM;
+        if (i < nseg) acc += (p.rows[i] + bm - 1) / bm;
         p.rg_end[i] = acc;
     }
     p.n_rg = acc;
@@ -460,10 +497,10 @@ void kq_groups(KqP &p, int nseg, const GroupTiles *grp) {
     }
 }
 
-template <bool GLU>
+template <bool GLU, int BN = KQ_BN>
 void kq_launch(const KqP &p, hipStream_t st) {
     const int slots = (p.n_rg + 7) / 8;
-    hipLaunchKernelGGL((gemm_q4k_kernel<GLU>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_q4k_kernel<GLU, BN>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
 void k6_launch(const KqP &p, hipStream_t st) {
@@ -496,8 +533,11 @@ bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, 
     p.qs = act.qs;
     p.d = act.d;
     p.bsums = act.bsums;
-    kq_groups(p, nseg, grp);
+    if (grp && grp->bn != KQ_BN && (grp->bn != 32 || ty != T_Q4_K)) return false;
+    const bool t32 = grp && grp->bn == 32;  // 32-token tiles of a Q4_K expert grouping
+    kq_groups(p, nseg, grp, t32 ? kq_bm<32>() : KQ_BM);
     if (ty == T_Q6_K) k6_launch(p, st);
+    else if (t32) kq_launch<false, 32>(p, st);
     else kq_launch<false>(p, st);
     return true;
 }
@@ -524,8 +564,11 @@ bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 
     p.qs = act.qs;
     p.d = act.d;
     p.bsums = act.bsums;
-    kq_groups(p, 1, grp);
-    kq_launch<true>(p, st);
+    if (grp && grp->bn != KQ_BN && grp->bn != 32) return false;
+    const bool t32 = grp && grp->bn == 32;  // 32-token tiles of a Q4_K expert grouping
+    kq_groups(p, 1, grp, t32 ? kq_bm<32>() : KQ_BM);
+    if (t32) kq_launch<true, 32>(p, st);
+    else kq_launch<true>(p, st);
     return true;
 }
 

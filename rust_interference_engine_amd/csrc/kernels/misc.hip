@@ -233,7 +233,7 @@ void launch_moe_shared_add(const float *ys, const float *gate_inp, const float *
 // each token's experts in ascending order from the pair index.  Expert ids outside
 // [0, n_exp) (only from non-finite router logits) are dropped.
 __global__ __launch_bounds__(1024) void moe_group_kernel(const int *__restrict__ sel, int n_pairs, int k, int n_exp, int *off,
-                                                         int *row_tok, int *row_slot, int *tile_e, int *tile_r0, int *n_tiles) {
+                                                         int *row_tok, int *row_slot, int *tile_e, int *tile_r0, int *n_tiles, int bn) {
     __shared__ int cnt[512], fill[512], base[513], tbase[513];
     const int tid = threadIdx.x;
     for (int e = tid; e < n_exp; e += 1024) {
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int *__restrict__
             base[e] = acc;
             tbase[e] = tacc;
             acc += cnt[e];
-            tacc += (cnt[e] + GROUP_BN - 1) / GROUP_BN;
+            tacc += (cnt[e] + bn - 1) / bn;
         }
         base[n_exp] = acc;
         tbase[n_exp] = tacc;
@@ -270,20 +270,20 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int *__restrict__
     for (int e = tid; e < n_exp; e += 1024)
         for (int i = 0; i < tbase[e + 1] - tbase[e]; i++) {
             tile_e[tbase[e] + i] = e;
-            tile_r0[tbase[e] + i] = base[e] + i * GROUP_BN;
+            tile_r0[tbase[e] + i] = base[e] + i * bn;
         }
 }
 
-int moe_group_max_tiles(int n_tok, int k, int n_exp) {
+int moe_group_max_tiles(int n_tok, int k, int n_exp, int bn) {
     // the full tiles of all pairs, plus at most one partial tile per expert that has rows
     const int pairs = n_tok * k;
-    return (pairs + GROUP_BN - 1) / GROUP_BN + std::min(n_exp, pairs);
+    return (pairs + bn - 1) / bn + std::min(n_exp, pairs);
 }
 
 void launch_moe_group(const int *sel, int n_tok, int k, int n_exp, int *off, int *row_tok, int *row_slot, int *tile_e, int *tile_r0,
-                      int *n_tiles, hipStream_t st) {
+                      int *n_tiles, int bn, hipStream_t st) {
     hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, st, sel, n_tok * k, k, n_exp, off, row_tok, row_slot, tile_e, tile_r0,
-                       n_tiles);
+                       n_tiles, bn);
 }
 
 void launch_moe_route(const float *logits, int n_tok, int n_exp, int k, int norm_topk, int unit_weights, int *sel, float *wgt,
