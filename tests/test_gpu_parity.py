@@ -394,6 +394,23 @@ def test_mixture_of_experts_matches_oracle(oracle, cuda, arch, ty, tol, mut):
         assert err < tol, f"{arch} {ty}: decode token {t}: {err}"
 
 
+@pytest.mark.parametrize("n_prompt", [70, 33])
+def test_moe_prompt_with_several_tiles_per_expert(oracle, cuda, n_prompt):
+    """A prompt whose experts each receive more than one 32-token tile of routed
+    tokens, the last one ragged (4 Q4_K experts, top-2: about n_prompt / 2 tokens
+    per expert), in one batch: every logits row against the oracle (cpu.rs:469-524)."""
+    from naive_model import max_rel_err
+
+    spec, g, o = _pair(oracle, "qwen3moe", Q4_K, 0, n_ctx=128, max_batch=80, mutate=MOE_MUTATIONS["mixtral"])
+    nv = spec.n_vocab
+    toks = [(i * 53 + 11) % nv for i in range(n_prompt)]
+    lg = g.forward(toks, 0, True)
+    lo = o.forward(toks, 0, True)
+    for t in range(n_prompt):
+        err = max_rel_err(lg[t * nv:(t + 1) * nv], lo[t * nv:(t + 1) * nv])
+        assert err < 0.03, f"prompt of {n_prompt}: token {t}: {err}"
+
+
 PROLOGUE_WIDTHS = {  # hidden sizes past one superblock / one 4096-value pass, and the 768-wide expert FFN
     None: None,
     "e2048_ff768": lambda s: [setattr(s, k, v) for k, v in (("n_embd", 2048), ("n_ff_exp", 768), ("n_ff", 1536))],
