@@ -230,6 +230,7 @@ HipBackend::HipBackend(const uint8_t *gguf, size_t len, const BackendConfig &cfg
     d_route_cnt_ = dalloc<int>(allocs_, 64);  // the router GEMV's arrival counter (one-token routing)
     d_amax_idx_ = dalloc<int>(allocs_, n_amax_part_);
     d_amax_val_ = dalloc<float>(allocs_, n_amax_part_);
+    d_amax_cnt_ = dalloc<int>(allocs_, 1);  // arrival counter of the one-launch argmax
     if (c.n_expert) {
         d_router_ = dalloc<float>(allocs_, mb * c.n_expert);
         d_moe_w_ = dalloc<float>(allocs_, mb * nu);
@@ -865,7 +866,7 @@ void HipBackend::greedy_step_graph(size_t pos) {
         try {
             run_layers(1, 0, d_pos_, false, ns);
             launch_argmax_step(d_logits_, (int)m_.cfg.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, d_gen_, d_pos_,
-                               (int)std::max<size_t>(n_ctx_, 1), st_);
+                               (int)std::max<size_t>(n_ctx_, 1), st_, d_amax_cnt_);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(st_, &g);
@@ -931,7 +932,7 @@ uint32_t HipBackend::forward_argmax(const uint32_t *tokens, size_t n, size_t pos
     } else {
         run_layers((int)n, pos, nullptr, false, splits_for(n, pos));
     }
-    launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
+    launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_, d_amax_cnt_);
     check_launch("argmax");
     uint32_t tok = 0;
     RIE_HIP_CHECK(hipMemcpyAsync(&tok, d_tokens_, 4, hipMemcpyDeviceToHost, st_));
@@ -967,7 +968,7 @@ void HipBackend::generate_greedy(size_t pos, size_t n_gen, uint32_t *out) {
         } else {
             run_layers(1, pos + i, nullptr, false, splits_for(1, pos + i));
         }
-        launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_);
+        launch_argmax(d_logits_, (int)c.n_vocab, d_amax_idx_, d_amax_val_, n_amax_part_, d_tokens_, st_, d_amax_cnt_);
         check_launch("argmax");
     }
     RIE_HIP_CHECK(hipMemcpyAsync(out, d_gen_, n_gen * 4, hipMemcpyDeviceToHost, st_));

@@ -128,7 +128,7 @@ class HipBackend {
     float *d_x_ = nullptr, *d_xn_ = nullptr, *d_q_ = nullptr, *d_k_ = nullptr, *d_v_ = nullptr, *d_att_ = nullptr, *d_h_ = nullptr,
           *d_o_ = nullptr, *d_logits_ = nullptr, *d_part_ = nullptr, *d_amax_val_ = nullptr, *d_gemm_ws_ = nullptr;
     size_t gemm_ws_cap_ = 0;  // floats at d_gemm_ws_
-    int *d_amax_idx_ = nullptr;
+    int *d_amax_idx_ = nullptr, *d_amax_cnt_ = nullptr;
     int *d_attn_cnt_ = nullptr;  // per-KV-head arrival counters of the fused single-token attention
     int *d_route_cnt_ = nullptr;  // arrival counter of the router GEMV that routes one token
     ActQ8 act0_, actk_;  // Q8_0 and Q8_K batches

@@ -329,15 +329,19 @@ int32_t rie_hip_k_moe_route(const float *logits, int32_t n_tok, int32_t n_exp, i
 
 int32_t rie_hip_k_argmax(const float *x, int32_t n, uint32_t *out_idx) {
     return guarded(nullptr, 0, [&] {
-        int *pi = nullptr;
-        float *pv = nullptr;
-        RIE_HIP_CHECK(hipMalloc(&pi, 64 * sizeof(int)));
-        RIE_HIP_CHECK(hipMalloc(&pv, 64 * sizeof(float)));
-        rie::launch_argmax(x, n, pi, pv, 64, out_idx, 0);
-        hipError_t e = hipGetLastError();
+        // 64 partial indices, 64 partial values and the arrival counter of the
+        // one-launch form (the backend's), in one zeroed allocation
+        void *buf = nullptr;
+        RIE_HIP_CHECK(hipMalloc(&buf, 129 * 4));
+        hipError_t e = hipMemset(buf, 0, 129 * 4);
+        if (e == hipSuccess) {
+            int *pi = (int *)buf;
+            float *pv = (float *)buf + 64;
+            rie::launch_argmax(x, n, pi, pv, 64, out_idx, 0, (int *)buf + 128);
+            e = hipGetLastError();
+        }
         hipError_t e2 = hipDeviceSynchronize();
-        (void)hipFree(pi);
-        (void)hipFree(pv);
+        (void)hipFree(buf);
         RIE_HIP_CHECK(e);
         RIE_HIP_CHECK(e2);
     });

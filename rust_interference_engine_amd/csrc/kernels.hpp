@@ -119,12 +119,15 @@ constexpr int ATT_MAX_SPLIT = 256;
 int attention_splits(int n_tok, int n_kv, int max_len, int hd, bool fused);
 
 // ---- misc.hip ----
-void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st);
+// cnt: one zeroed int (left zeroed) for the one-launch form, where the last workgroup
+// reduces the partials; nullptr: two launches
+void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st,
+                   int *cnt = nullptr);
 // The same, as one step of greedy decoding replayed in a graph: the token also goes
 // to gen[step[1] + 1] (when below gen_cap), then step[0] (position) and step[1]
 // (index of the step) advance by one.
 void launch_argmax_step(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, uint32_t *gen,
-                        int *step, int gen_cap, hipStream_t st);
+                        int *step, int gen_cap, hipStream_t st, int *cnt = nullptr);
 // The same argmax with its partials in the library's static device array (no
 // allocation); n in 1..ARGMAX_SCRATCH_PARTS·ARGMAX_SCRATCH_PER_PART, else throws.
 // Calls that overlap on one GPU share the array and race.

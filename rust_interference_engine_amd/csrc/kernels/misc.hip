@@ -68,13 +68,79 @@ __global__ __launch_bounds__(64) void argmax_stage2(const int *pidx, const float
     }
 }
 
-void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st) {
+// Both stages in one launch: every workgroup stores its partial with agent-scope
+// atomic stores (written through to the device coherence point), waits for their
+// completion, and counts its arrival with a relaxed agent-scope add; the last
+// workgroup to arrive re-arms the counter and reduces the partials in its first
+// wave with agent-scope atomic loads, in partial order (the first strict maximum,
+// as argmax_stage2).  No release or acquire, which would write back or invalidate
+// the whole L2 of the XCD.
+__global__ __launch_bounds__(256) void argmax_one_kernel(const float *__restrict__ x, int n, int *pidx, float *pval, int *cnt, uint32_t *out,
+                                                         uint32_t *gen, int *step, int gen_cap) {
+    const int tid = threadIdx.x;
+    const int per = (n + gridDim.x - 1) / gridDim.x;
+    const int a = blockIdx.x * per, b = min(n, a + per);
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = a + tid; i < b; i += 256) {
+        const float xv = x[i];
+        if (xv > v) {
+            v = xv;
+            idx = i;
+        }
+    }
+    xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ int s_last;
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = v;
+        si[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; w++) amax_merge(v, idx, sv[w], si[w]);
+        st_coh(pval + blockIdx.x, v);
+        __hip_atomic_store(pidx + blockIdx.x, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vmem();
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (int)gridDim.x - 1;
+        if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last || tid >= 64) return;
+    v = -INFINITY;
+    idx = 0x7fffffff;
+    for (int i = tid; i < (int)gridDim.x; i += 64)
+        amax_merge(v, idx, ld_coh(pval + i), __hip_atomic_load(pidx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    xor_down<32, 1>([&](auto o) { amax_merge(v, idx, xor_f<decltype(o)::value>(v), xor_i<decltype(o)::value>(idx)); });
+    if (tid == 0) {
+        const uint32_t t = idx == 0x7fffffff ? 0u : (uint32_t)idx;
+        *out = t;
+        if (gen) {
+            const int g = step[1] + 1;
+            if (g < gen_cap) gen[g] = t;
+            step[1] = g;
+            step[0] += 1;
+        }
+    }
+}
+
+void launch_argmax(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, hipStream_t st, int *cnt) {
+    if (cnt) {
+        hipLaunchKernelGGL(argmax_one_kernel, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val, cnt, out_idx, nullptr, nullptr, 0);
+        return;
+    }
     hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
     hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx, nullptr, nullptr, 0);
 }
 
 void launch_argmax_step(const float *x, int n, int *partial_idx, float *partial_val, int n_part, uint32_t *out_idx, uint32_t *gen,
-                        int *step, int gen_cap, hipStream_t st) {
+                        int *step, int gen_cap, hipStream_t st, int *cnt) {
+    if (cnt) {
+        hipLaunchKernelGGL(argmax_one_kernel, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val, cnt, out_idx, gen, step, gen_cap);
+        return;
+    }
     hipLaunchKernelGGL(argmax_stage1, dim3(n_part), dim3(256), 0, st, x, n, partial_idx, partial_val);
     hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, partial_idx, partial_val, n_part, out_idx, gen, step, gen_cap);
 }
