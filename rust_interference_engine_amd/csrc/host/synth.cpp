@@ -437,7 +437,7 @@ int32_t synth_preset(const char *name, int32_t wtype, rie_hip_synth_spec *s) {
         {"phi-4-mini", "phi3", 200064, 3072, 32, 24, 8, 128, 8192, 1},
         {"smollm2-360m", "llama", 49152, 960, 32, 15, 5, 64, 2560, 1},
         {"qwen3-30b-a3b", "qwen3moe", 151936, 2048, 48, 32, 4, 128, 6144, 0},
-        // BASELINE workload shapes that are not presets of the reference
+        // benchmark workload shapes that are not presets of the reference
         {"llama-3.1-8b", "llama", 128256, 4096, 32, 32, 8, 128, 14336, 0},
     };
     for (const P &p : presets) {
