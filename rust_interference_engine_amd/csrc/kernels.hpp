@@ -185,7 +185,12 @@ int moe_group_max_tiles(int n_tok, int k, int n_exp, int bn = GROUP_BN);
 
 // ---- gemm_kq.hip (prefill, Q4_K × Q8_K on int8 MFMA; reached through gemm.hip) ----
 bool gemm_kq_supported(int ty, size_t K);
-bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr);
+// part (part_cap floats): partial sums of a K split (Q6_K, one ungrouped segment)
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp = nullptr,
+                    float *part = nullptr, size_t part_cap = 0);
+// out[t·ld + r] += part[0][t·ld + r] + … + part[n_part−1][…] (planes stride floats
+// apart) for r < rows, t < n_tok, in split order
+void launch_gemm_add_parts(float *out, const float *part, size_t stride, int n_part, int rows, int ld, int n_tok, hipStream_t st);
 bool launch_gemm_kq_glu(const DevWeight &gate, const DevWeight &up, const ActQ8 &act, int n_tok, int K, float *h, int ld, int gelu,
                         hipStream_t st, const GroupTiles *grp = nullptr);
 

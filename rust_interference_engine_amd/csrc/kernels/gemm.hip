@@ -400,6 +400,10 @@ static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp, float *part
     hipLaunchKernelGGL((gemm_kernel<TY, GLU, 1>), grid, dim3(256), 0, st, p);
 }
 
+void launch_gemm_add_parts(float *out, const float *part, size_t stride, int n_part, int rows, int ld, int n_tok, hipStream_t st) {
+    hipLaunchKernelGGL(gemm_add_parts_kernel, dim3((rows + 255) / 256, n_tok), dim3(256), 0, st, out, part, stride, n_part, rows, ld);
+}
+
 static bool operands_ok(const ActQ8 &act) { return act.qs && act.d; }
 
 static void set_groups(GemmP &p, int nseg) {
@@ -415,7 +419,7 @@ bool launch_gemm(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int
                  size_t part_cap) {
     if (nseg < 1 || nseg > 3 || n_tok < 1 || !operands_ok(act) || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
-    if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st, grp);
+    if (gemm_kq_supported(ty, K)) return launch_gemm_kq(segs, nseg, act, n_tok, K, st, grp, part, part_cap);
     if (grp && grp->bn != GROUP_BN) return false;  // this kernel's grouped tiles are 64 tokens
     GemmP p{};
     for (int i = 0; i < nseg; i++) {

@@ -60,6 +60,13 @@ struct KqP {
     int n_tok, K;
     int grouped;     // expert groups: one matrix per expert (grp), token tiles from its table
     GroupTiles grp;
+    // K split (Q6_K, one segment, not grouped): split i takes superblocks
+    // [i·nsb/ks, (i+1)·nsb/ks); split 0 runs the segment's epilogue on its partial
+    // sum, split i > 0 stores its partial to part[i-1] ([n_tok][ld], stride
+    // part_stride floats), which a second launch adds to the output in split order
+    int ks;
+    float *part;
+    size_t part_stride;
 };
 
 constexpr int KQ_BM = 64, KQ_BN = 64;
@@ -411,8 +418,11 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     __shared__ K6Stage st[2];
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
     const int wr = wv >> 1, wc = wv & 1;
-    const int bid = blockIdx.x;  // workgroups of one row group share an XCD (id mod 8)
-    const int xcd = bid & 7, u = bid >> 3;
+    // workgroups of one row group share an XCD (id mod 8); the K splits of one tile
+    // are neighbours in u (the same XCD)
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, uk = bid >> 3;
+    const int ksi = uk % p.ks, u = uk / p.ks;
     const int tg = u % p.n_tg;
     const int rg = (u / p.n_tg) * 8 + xcd;
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
@@ -436,14 +446,17 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
         acc[v] = 0.0f;
         s1[v] = 0;
     }
-    const int n_stages = (p.K >> 8) * 2;
+    // this workgroup's superblocks [sb0, sb0 + n_stages / 2) (its K split)
+    const int nsb = p.K >> 8;
+    const int sb0 = ksi * nsb / p.ks;
+    const int n_stages = ((ksi + 1) * nsb / p.ks - sb0) * 2;
     K6Regs R;
-    k6_load(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
+    k6_load(p, sg, row0, tokA, tokD, woff, sb0, 0, tid, R);
     k6_store(st[0], tid, R);
     __syncthreads();
     for (int s = 0; s < n_stages; s++) {
         const int hs = s & 1;
-        if (s + 1 < n_stages) k6_load(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        if (s + 1 < n_stages) k6_load(p, sg, row0, tokA, tokD, woff, sb0 + ((s + 1) >> 1), (s + 1) & 1, tid, R);
         const K6Stage &S = st[s & 1];
 #pragma unroll
         for (int k = 0; k < 8; k++) {  // 16-value sub-blocks of the half
@@ -468,9 +481,9 @@ __global__ __launch_bounds__(256) void gemm_q6k_kernel(KqP p) {
     const int rows = p.rows[sg];
     const int row = row0 + wrow;
     if (row >= rows) return;
-    float *out = p.out[sg];
+    float *out = ksi ? p.part + (size_t)(ksi - 1) * p.part_stride : p.out[sg];
     const int ld = p.ld[sg];
-    const int epi = p.epi[sg];
+    const int epi = ksi ? EPI_STORE : p.epi[sg];
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int r = tr.r0 + wc * 32 + 16 * h + v;
@@ -503,16 +516,29 @@ void kq_launch(const KqP &p, hipStream_t st) {
     hipLaunchKernelGGL((gemm_q4k_kernel<GLU, BN>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
 }
 
-void k6_launch(const KqP &p, hipStream_t st) {
+// A single ungrouped segment whose tiles number under 512 splits K in 2 or 4
+// (each split ≥ 4 superblocks) while part holds the extra splits' partial sums
+// (part_cap floats); the partials are added by a second launch.
+void k6_launch(KqP p, hipStream_t st, float *part, size_t part_cap) {
     const int slots = (p.n_rg + 7) / 8;
-    hipLaunchKernelGGL(gemm_q6k_kernel, dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    const int tiles = slots * 8 * p.n_tg, nsb = p.K >> 8;
+    p.ks = 1;
+    if (!p.grouped && p.nseg == 1 && part && p.n_tok > 64) {
+        const size_t plane = (size_t)p.n_tok * p.ld[0];
+        while (p.ks < 4 && tiles * p.ks < 512 && nsb / (2 * p.ks) >= 4 && (size_t)(2 * p.ks - 1) * plane <= part_cap) p.ks *= 2;
+        p.part = part;
+        p.part_stride = plane;
+    }
+    hipLaunchKernelGGL(gemm_q6k_kernel, dim3(tiles * p.ks), dim3(256), 0, st, p);
+    if (p.ks > 1) launch_gemm_add_parts(p.out[0], p.part, p.part_stride, p.ks - 1, p.rows[0], p.ld[0], p.n_tok, st);
 }
 
 }  // namespace
 
 bool gemm_kq_supported(int ty, size_t K) { return (ty == T_Q4_K || ty == T_Q6_K) && K % 256 == 0 && K > 0; }
 
-bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp) {
+bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, int K, hipStream_t st, const GroupTiles *grp, float *part,
+                    size_t part_cap) {
     if (nseg < 1 || nseg > 3 || n_tok < 1 || !act.qs || !act.d || (grp && (nseg != 1 || grp->max_tiles < 1))) return false;
     const int ty = segs[0].w.ty;
     if (ty == T_Q4_K && !act.bsums) return false;
@@ -536,7 +562,7 @@ bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, 
     if (grp && grp->bn != KQ_BN && (grp->bn != 32 || ty != T_Q4_K)) return false;
     const bool t32 = grp && grp->bn == 32;  // 32-token tiles of a Q4_K expert grouping
     kq_groups(p, nseg, grp, t32 ? kq_bm<32>() : KQ_BM);
-    if (ty == T_Q6_K) k6_launch(p, st);
+    if (ty == T_Q6_K) k6_launch(p, st, part, part_cap);
     else if (t32) kq_launch<false, 32>(p, st);
     else kq_launch<false>(p, st);
     return true;
