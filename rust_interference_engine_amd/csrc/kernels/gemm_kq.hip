@@ -222,8 +222,12 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     __shared__ KqStage<GLU, BN> st[2];
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
     const int wr = wv / WC, wc = wv % WC;
-    const int bid = blockIdx.x;  // workgroups of one row group share an XCD (id mod 8)
-    const int xcd = bid & 7, u = bid >> 3;
+    // workgroups of one row group share an XCD (id mod 8); the K splits of one tile
+    // (non-gated 64-token tiles only) are neighbours in u (the same XCD)
+    constexpr bool KSPLIT = !GLU && BN == 64;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, uk = bid >> 3;
+    const int ksi = KSPLIT ? uk % p.ks : 0, u = KSPLIT ? uk / p.ks : uk;
     const int tg = u % p.n_tg;
     const int rg = (u / p.n_tg) * 8 + xcd;
     if (rg >= p.n_rg) return;  // whole workgroup: uniform
@@ -251,14 +255,17 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
             acc[a][v] = 0.0f;
             s1[a][v] = 0;
         }
-    const int n_stages = (p.K >> 8) * 2;
+    // this workgroup's superblocks [sb0, sb0 + n_stages / 2) (its K split)
+    const int nsb = p.K >> 8;
+    const int sb0 = KSPLIT ? ksi * nsb / p.ks : 0;
+    const int n_stages = KSPLIT ? ((ksi + 1) * nsb / p.ks - sb0) * 2 : nsb * 2;
     KqRegs<GLU, BN> R;
-    kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, 0, 0, tid, R);
+    kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, sb0, 0, tid, R);
     kq_store<GLU, BN>(st[0], tid, R);
     __syncthreads();
     for (int s = 0; s < n_stages; s++) {
         const int hs = s & 1;
-        if (s + 1 < n_stages) kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, (s + 1) >> 1, (s + 1) & 1, tid, R);
+        if (s + 1 < n_stages) kq_load<GLU, BN>(p, sg, row0, tokA, tokD, woff, sb0 + ((s + 1) >> 1), (s + 1) & 1, tid, R);
         const KqStage<GLU, BN> &S = st[s & 1];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -311,9 +318,9 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(KqP p) {
     const int rows = p.rows[sg];
     const int row = row0 + wrow;
     if (row >= rows) return;
-    float *out = p.out[sg];
+    float *out = (KSPLIT && ksi) ? p.part + (size_t)(ksi - 1) * p.part_stride : p.out[sg];
     const int ld = p.ld[sg];
-    const int epi = p.epi[sg];
+    const int epi = (KSPLIT && ksi) ? EPI_STORE : p.epi[sg];
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int r = tr.r0 + wc * 32 + 16 * h + v;
@@ -510,10 +517,20 @@ void kq_groups(KqP &p, int nseg, const GroupTiles *grp, int bm = KQ_BM) {
     }
 }
 
+// The non-gated 64-token form splits K as k6_launch does (below).
 template <bool GLU, int BN = KQ_BN>
-void kq_launch(const KqP &p, hipStream_t st) {
+void kq_launch(KqP p, hipStream_t st, float *part = nullptr, size_t part_cap = 0) {
     const int slots = (p.n_rg + 7) / 8;
-    hipLaunchKernelGGL((gemm_q4k_kernel<GLU, BN>), dim3(slots * 8 * p.n_tg), dim3(256), 0, st, p);
+    const int tiles = slots * 8 * p.n_tg, nsb = p.K >> 8;
+    p.ks = 1;
+    if (!GLU && BN == 64 && !p.grouped && p.nseg == 1 && part && p.n_tok > 64) {
+        const size_t plane = (size_t)p.n_tok * p.ld[0];
+        while (p.ks < 4 && tiles * p.ks < 512 && nsb / (2 * p.ks) >= 4 && (size_t)(2 * p.ks - 1) * plane <= part_cap) p.ks *= 2;
+        p.part = part;
+        p.part_stride = plane;
+    }
+    hipLaunchKernelGGL((gemm_q4k_kernel<GLU, BN>), dim3(tiles * p.ks), dim3(256), 0, st, p);
+    if (p.ks > 1) launch_gemm_add_parts(p.out[0], p.part, p.part_stride, p.ks - 1, p.rows[0], p.ld[0], p.n_tok, st);
 }
 
 // A single ungrouped segment whose tiles number under 512 splits K in 2 or 4
@@ -564,7 +581,7 @@ bool launch_gemm_kq(const GemvSeg *segs, int nseg, const ActQ8 &act, int n_tok, 
     kq_groups(p, nseg, grp, t32 ? kq_bm<32>() : KQ_BM);
     if (ty == T_Q6_K) k6_launch(p, st, part, part_cap);
     else if (t32) kq_launch<false, 32>(p, st);
-    else kq_launch<false>(p, st);
+    else kq_launch<false>(p, st, part, part_cap);
     return true;
 }
 

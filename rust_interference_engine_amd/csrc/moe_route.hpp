@@ -24,6 +24,13 @@ __device__ __forceinline__ float row_max16(float v) {
     v = fmaxf(v, dpp_f<DPP_ROW_ROR4>(v));
     return fmaxf(v, dpp_f<DPP_ROW_ROR8>(v));
 }
+// e^x rounded once to f32: the double-precision exponential is far more accurate
+// than the half-ulp f32 rounding, so this is glibc's expf (the reference's f32::exp,
+// within 0.502 ulp of e^x) but for inputs within ~0.002 ulp of a rounding midpoint,
+// also through the subnormal range, where the device's f32 exponential flushes e^x
+// near 2^-149 to zero.
+__device__ __forceinline__ float exp_f32_rn(float x) { return (float)exp((double)x); }
+
 // One wavefront routes one token: l holds its n_exp logits; sel/wgt receive its k
 // choices in ascending expert order.  NE = experts per lane (n_exp ≤ 64·NE).
 // COH: the logits were published by other workgroups of the same launch with
@@ -40,8 +47,24 @@ __device__ __forceinline__ void moe_route_wave_t(const float *l, int n_exp, int 
         mx = fmaxf(mx, pr[i]);
     }
     mx = wave_max(mx, 64);
+    // The reference ranks the f32 probabilities as they round (ties by index), so a
+    // token whose k-th place lies in the subnormal range (a peaked softmax: fewer
+    // than k probabilities safely normal after the division by the sum ≤ 128) takes
+    // its experts by how e^x rounds there; that wave computes its exponentials
+    // again, rounded once from double (exp_f32_rn).  Elsewhere the f32 exponential
+    // decides as before.
+    float xs[NE];
+    int normal = 0;
 #pragma unroll
-    for (int i = 0; i < NE; i++) pr[i] = lane + 64 * i < n_exp ? expf(pr[i] - mx) : 0.0f;
+    for (int i = 0; i < NE; i++) {
+        xs[i] = pr[i] - mx;
+        pr[i] = lane + 64 * i < n_exp ? expf(xs[i]) : 0.0f;
+        normal += __popcll(__ballot(pr[i] >= 0x1p-120f));
+    }
+    if (normal < k) {
+#pragma unroll
+        for (int i = 0; i < NE; i++) pr[i] = lane + 64 * i < n_exp ? exp_f32_rn(xs[i]) : 0.0f;
+    }
     // the sum over the experts in order, one add at a time (expert e sits in lane
     // e mod 64, register e / 64): the same chain in every lane, through readlane;
     // the zeros past n_exp add nothing

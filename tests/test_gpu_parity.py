@@ -184,7 +184,7 @@ def test_gemm_matches_oracle_rows(oracle, cuda, ty):
         shapes += ((8320, 96, 200), (14336, 64, 130))
     if ty in (Q4_K, Q6_K):
         shapes = ((256, 40, 9), (512, 200, 33), (4096, 96, 70), (1024, 300, 130), (8192, 64, 512))
-    if ty == Q6_K:  # K split: 13 superblocks in two uneven splits (6 and 7)
+    if ty in (Q4_K, Q6_K):  # K split: 13 superblocks in two uneven splits (6 and 7)
         shapes += ((3328, 96, 70),)
     for k, rows, n_tok in shapes:
         w = r.random_weight(ty, rows, k)
