@@ -301,9 +301,9 @@ int32_t rie_hip_k_gemm(int32_t ty, const uint8_t *w, int32_t rows, int32_t k, co
         rie::GemvSeg sg{mkw(ty, pw.data, rows, k), out, rows, rie::EPI_STORE};
         // room for the partial sums of a K split (up to three planes, capped at
         // 64 MiB like the backend's workspace), only where a split can happen:
-        // Q4_0/Q8_0 weights with at least 64 stages of 128 values, or Q4_K/Q6_K with
+        // Q4_0/Q8_0 weights with at least 48 stages of 128 values, or Q4_K/Q6_K with
         // at least 8 superblocks, over 64 tokens
-        const bool can_split = ((ty == rie::T_Q4_0 || ty == rie::T_Q8_0) && k / 128 >= 64 && n_tok > 64) ||
+        const bool can_split = ((ty == rie::T_Q4_0 || ty == rie::T_Q8_0) && k / 128 >= 48 && n_tok > 64) ||
                                ((ty == rie::T_Q4_K || ty == rie::T_Q6_K) && k / 256 >= 8 && n_tok > 64);
         const size_t cap = can_split ? std::min<size_t>(3 * (size_t)n_tok * (size_t)std::max(rows, 0), (size_t)1 << 24) : 0;
         float *part = nullptr;

@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256) void gemm_add_parts_kernel(float *__restrict__
 
 // 128-token tiles unless that leaves fewer than two workgroups per CU (256 CUs),
 // then 64-token tiles (one 32-token tile per wave); the gated pair always 64.
-// One segment with a long K (≥ 64 stages of 128) whose 128-token tiles number
+// One segment with a long K (≥ 48 stages of 128) whose 128-token tiles number
 // under 512 keeps the 128-token tiles and splits K in 2 or 4 (each split ≥ 16
 // stages) while part holds the extra splits' partial sums (part_cap floats).
 template <int TY, bool GLU>
@@ -372,7 +372,7 @@ static void launch_t(GemmP p, hipStream_t st, const GroupTiles *grp, float *part
     const int tiles128 = slots * 8 * ((p.n_tok + 127) / 128);
     const int n_st = p.K / (32 * G_KC);
     p.ks = 1;
-    if (!GLU && !grp && p.nseg == 1 && part && n_st >= 64 && p.n_tok > 64) {
+    if (!GLU && !grp && p.nseg == 1 && part && n_st >= 48 && p.n_tok > 64) {
         const size_t plane = (size_t)p.n_tok * p.ld[0];
         while (p.ks < 4 && tiles128 * p.ks < 512 && n_st / (2 * p.ks) >= 16 && (size_t)(2 * p.ks - 1) * plane <= part_cap) p.ks *= 2;
         p.part = part;

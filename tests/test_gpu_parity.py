@@ -180,8 +180,9 @@ def test_gemm_matches_oracle_rows(oracle, cuda, ty):
     shapes = ((128, 40, 9), (256, 200, 33), (4096, 96, 70), (1024, 300, 130))
     if ty in (Q4_0, Q8_0):
         # long K over few tiles: K split in four (65 stages of 128: splits of 16,
-        # 16, 16 and 17 stages; 112 stages with a partial 128-token tile)
-        shapes += ((8320, 96, 200), (14336, 64, 130))
+        # 16, 16 and 17 stages; 112 stages with a partial 128-token tile), and in
+        # two (48 stages, the shortest K that splits)
+        shapes += ((8320, 96, 200), (14336, 64, 130), (6144, 96, 130))
     if ty in (Q4_K, Q6_K):
         shapes = ((256, 40, 9), (512, 200, 33), (4096, 96, 70), (1024, 300, 130), (8192, 64, 512))
     if ty in (Q4_K, Q6_K):  # K split: 13 superblocks in two uneven splits (6 and 7)
